@@ -1,0 +1,107 @@
+/*
+ * sa.h -- C ABI of the MI355X (gfx950) Selective Attention kernels.
+ *
+ * Selective Attention (Leviathan, Kalman, Matias, ICLR 2025): causal softmax attention whose
+ * logits, for every head h, have the running selection F subtracted:
+ *
+ *     L_h[i,j] = s q_h[i].k_h[j]                     s = 1/sqrt(D), key j <= query i
+ *     S[r,j]   = relu(L_0[r,j])   if E <= j < r, else 0      (head 0 of the sequence selects)
+ *     F[i,j]   = sum_{r<i} S[r,j]
+ *     O_h      = softmax_j(L_h - F) V_h
+ *
+ * Every entry point takes plain device pointers, sizes and a hipStream_t (passed as void*),
+ * never allocates, never throws, and returns an int status (0 = ok, < 0 = error; see
+ * sa_status_string). The caller owns every buffer. Launches are asynchronous on `stream`.
+ *
+ * Tensor layouts (row-major, contiguous):
+ *   q, k, v, dout            (nseq*heads, T, D)      storage dtype SA_DTYPE_BF16 or SA_DTYPE_F32
+ *   out                      (nseq*heads, Tq, D)     fp32
+ *   rmax, rden               (nseq*heads, Tq)        fp32   row max (log2 domain) / denominator
+ *   carry                    (nseq, ceil(Tq/32), Tk) fp32   per-key selection on entry to every
+ *                                                           32-query block (the reference's CARRY)
+ *   state_in / state_out     (nseq, state_ld)        fp32   per-key selection before / after
+ * The operand precision follows the storage dtype: bf16 storage runs bf16 MFMA with fp32
+ * accumulation; fp32 storage runs fp32 MFMA. Selection, F, softmax statistics and every
+ * accumulator are fp32.
+ *
+ * Per-head selection (every head its own selector) is the caller reshaping (B, H, T, D) to
+ * nseq = B*H sequences of heads = 1, as the reference's module does (mixers.py:76-84).
+ */
+#ifndef SA_H
+#define SA_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define SA_DTYPE_BF16 0
+#define SA_DTYPE_F32 1
+
+#define SA_OK 0
+#define SA_ERR_ARGUMENT -1      /* a size, pointer or option is invalid */
+#define SA_ERR_HEAD_DIM -2      /* head_dim not in {32, 64, 128} */
+#define SA_ERR_DTYPE -3         /* dtype code unknown */
+#define SA_ERR_WORKSPACE -4     /* workspace smaller than the *_workspace_bytes figure */
+#define SA_ERR_LAUNCH -5        /* a kernel launch failed (hipGetLastError) */
+
+/* ABI revision of this header; bumps when a signature changes. */
+int sa_abi_version(void);
+
+/* Human-readable text for a status code (static storage). */
+const char* sa_status_string(int status);
+
+/* Leading dimension (elements) of the transposed copies held in the workspaces. */
+int64_t sa_transposed_ld(int64_t t);
+
+/* Bytes of scratch sa_forward needs (the transposed value copy). */
+int64_t sa_forward_workspace_bytes(int64_t nseq, int64_t heads, int64_t tk, int64_t head_dim, int dtype);
+
+/*
+ * Forward pass, and one chunk of a chunked prefill.
+ *
+ * Replaces selective_attention_forward's two Triton launches (_selective_carry and
+ * _selective_forward[_grouped]), reference src/selective_attention/kernels.py:526-605, and
+ * adds the chunk form the reference lacks: queries are the absolute positions
+ * [q_offset, q_offset + tq) of a sequence whose keys/values are [0, tk), tk = q_offset + tq.
+ * state_in (may be NULL when q_offset == 0) holds, for every key j < q_offset, the selection
+ * sum over all queries before q_offset; state_out receives the same sum over all queries
+ * before q_offset + tq (for q_offset == 0 it is the reference's `selected_total`,
+ * kernels.py:547-549). state_in and state_out may alias.
+ *
+ * scale: the logit scale s (the reference uses 1/sqrt(D); a caller that zero-pads D passes the
+ * unpadded value). group: heads per wavefront (0 = automatic); damp_mode 0 none, 1 linear, 2 sqrt scales F of
+ * query i by min(1, train_len/(i+1)) (or its square root), reference kernels.py:179-182.
+ */
+int sa_forward(const void* q, const void* k, const void* v,
+               float* out, float* rmax, float* rden, float* carry,
+               const float* state_in, float* state_out, int64_t state_ld,
+               void* workspace, int64_t workspace_bytes,
+               int64_t nseq, int64_t heads, int64_t tq, int64_t tk, int64_t q_offset,
+               int64_t head_dim, float scale, int dtype, int exempt, int group,
+               int damp_mode, int64_t train_len, void* stream);
+
+/* Bytes of scratch sa_backward needs. */
+int64_t sa_backward_workspace_bytes(int64_t nseq, int64_t heads, int64_t t, int64_t head_dim, int dtype);
+
+/*
+ * Full backward pass: replaces _SelectiveAttentionFn.backward (dbar, zeroing, the
+ * _selective_backward[_pair] launch and the head-0 merge), reference
+ * src/selective_attention/kernels.py:621-666. Inputs are those of a full forward
+ * (q_offset 0, tq == tk == t) plus its out, rmax, rden and carry, and dout in the storage
+ * dtype. dq, dk, dv receive the gradients in the storage dtype, head 0's selection path
+ * included.
+ */
+int sa_backward(const void* q, const void* k, const void* v, const float* out, const void* dout,
+                const float* rmax, const float* rden, const float* carry,
+                void* dq, void* dk, void* dv,
+                void* workspace, int64_t workspace_bytes,
+                int64_t nseq, int64_t heads, int64_t t, int64_t head_dim, float scale, int dtype,
+                int exempt, int group, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* SA_H */

@@ -1,0 +1,11 @@
+#!/usr/bin/env bash
+# Builds libsa_hip.so (gfx950) next to the Python package. Run from anywhere.
+set -euo pipefail
+here="$(cd "$(dirname "${BASH_SOURCE[0]}")" && pwd)"
+root="$(cd "$here/../.." && pwd)"
+out="$here/../selective_attention/libsa_hip.so"
+hipcc --offload-arch=gfx950 -O3 -std=c++17 -fPIC -shared -munsafe-fp-atomics \
+  -Xclang -target-feature -Xclang -packed-fp32-ops \
+  -I"$root/include" "$here/sa_kernels.hip" -o "$out.tmp"
+mv "$out.tmp" "$out"
+echo "built $out"

@@ -1,0 +1,82 @@
+"""ctypes binding of the C ABI in include/sa.h (libsa_hip.so, built in-tree next to this file).
+
+The library is loaded once per process. Nothing here falls back to another implementation: when
+the shared object is missing or fails to load, `load()` raises RuntimeError with the reason, and
+the operator entry points in `kernels` refuse to run.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import os
+import threading
+
+LIB_NAME = "libsa_hip.so"
+LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), LIB_NAME)
+
+DTYPE_BF16 = 0
+DTYPE_F32 = 1
+
+# Every function the header declares, with its ctypes signature.
+_P = ctypes.c_void_p
+_I64 = ctypes.c_int64
+_I = ctypes.c_int
+_F = ctypes.c_float
+SIGNATURES = {
+    "sa_abi_version": (_I, []),
+    "sa_status_string": (ctypes.c_char_p, [_I]),
+    "sa_transposed_ld": (_I64, [_I64]),
+    "sa_forward_workspace_bytes": (_I64, [_I64, _I64, _I64, _I64, _I]),
+    "sa_forward": (_I, [_P, _P, _P, _P, _P, _P, _P, _P, _P, _I64, _P, _I64,
+                        _I64, _I64, _I64, _I64, _I64, _I64, _F, _I, _I, _I, _I, _I64, _P]),
+    "sa_backward_workspace_bytes": (_I64, [_I64, _I64, _I64, _I64, _I]),
+    "sa_backward": (_I, [_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _I64,
+                         _I64, _I64, _I64, _I64, _F, _I, _I, _I, _P]),
+}
+
+_lock = threading.Lock()
+_lib = None
+_error: str | None = None
+
+
+def load() -> ctypes.CDLL:
+    """The loaded library; RuntimeError when it cannot be loaded."""
+
+    global _lib, _error
+    with _lock:
+        if _lib is not None:
+            return _lib
+        if _error is not None:
+            raise RuntimeError(_error)
+        if not os.path.exists(LIB_PATH):
+            _error = (f"the HIP kernel library {LIB_PATH} is not built "
+                      "(run __graft_entry__.build() or selective-attention-study_amd/csrc/build.sh)")
+            raise RuntimeError(_error)
+        try:
+            lib = ctypes.CDLL(LIB_PATH)
+        except OSError as exc:  # missing ROCm runtime, wrong architecture, ...
+            _error = f"cannot load {LIB_PATH}: {exc}"
+            raise RuntimeError(_error) from exc
+        for name, (res, args) in SIGNATURES.items():
+            fn = getattr(lib, name)
+            fn.restype = res
+            fn.argtypes = args
+        _lib = lib
+        return lib
+
+
+def available() -> bool:
+    try:
+        load()
+    except RuntimeError:
+        return False
+    return True
+
+
+def check(status: int) -> None:
+    """Raise RuntimeError for a non-zero status from the C ABI."""
+
+    if status != 0:
+        lib = load()
+        raise RuntimeError(f"selective attention HIP call failed ({status}): "
+                           f"{lib.sa_status_string(status).decode()}")

@@ -1,0 +1,101 @@
+"""The C ABI library (no GPU needed): it loads, exports every entry point include/sa.h declares, and
+its host-side sizing/validation entry points behave; the Python API's input checks run on the CPU."""
+
+from __future__ import annotations
+
+import ctypes
+import os
+import re
+
+import pytest
+import torch
+
+from selective_attention import _lib, kernels
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "sa.h")
+
+
+def _declared():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(sa_[a-z_0-9]+)\s*\(", text)))
+
+
+def test_header_declares_the_bound_functions():
+    assert _declared() == sorted(_lib.SIGNATURES)
+
+
+def test_library_loads_and_exports_every_declared_symbol():
+    lib = _lib.load()
+    for name in _declared():
+        assert hasattr(lib, name), name
+    assert lib.sa_abi_version() >= 1
+
+
+def test_status_strings():
+    lib = _lib.load()
+    for code in (0, -1, -2, -3, -4, -5):
+        assert lib.sa_status_string(code)
+    assert b"head_dim" in lib.sa_status_string(-2)
+
+
+def test_workspace_sizes():
+    lib = _lib.load()
+    assert lib.sa_transposed_ld(1) == 64 and lib.sa_transposed_ld(64) == 64 and lib.sa_transposed_ld(65) == 128
+    fw = lib.sa_forward_workspace_bytes(1, 16, 16384, 64, 0)
+    assert fw >= 16 * 64 * 16384 * 2 and fw % 256 == 0
+    bw = lib.sa_backward_workspace_bytes(1, 16, 16384, 64, 0)
+    assert bw >= 16 * 16384 * 64 * 4 * 3    # dq, dk, dv fp32 at least
+
+
+def test_invalid_arguments_are_rejected_before_any_launch():
+    """Host validation in C: no pointer is dereferenced, no kernel launched."""
+    lib = _lib.load()
+    fake = 1 << 20   # never dereferenced: validation fails first
+    args = [fake] * 9 + [16, fake, 1 << 30, 1, 4, 16, 16, 0, 64, 0.125, 0, 1, 0, 0, 0, None]
+    bad = list(args)
+    bad[16] = 5          # q_offset + tq != tk
+    assert lib.sa_forward(*bad) == -1
+    bad = list(args)
+    bad[17] = 48         # head_dim
+    assert lib.sa_forward(*bad) == -2
+    bad = list(args)
+    bad[19] = 7          # dtype
+    assert lib.sa_forward(*bad) == -3
+    bad = list(args)
+    bad[11] = 16         # workspace too small
+    assert lib.sa_forward(*bad) == -4
+    bad = list(args)
+    bad[20] = 0          # exempt
+    assert lib.sa_forward(*bad) == -1
+    bargs = [fake] * 12 + [1 << 30, 1, 4, 16, 64, 0.125, 0, 1, 0, None]
+    bad = list(bargs)
+    bad[16] = 100
+    assert lib.sa_backward(*bad) == -2
+    bad = list(bargs)
+    bad[17] = -1.0
+    assert lib.sa_backward(*bad) == -1
+
+
+def test_api_checks_on_cpu_tensors():
+    q = torch.randn(1, 2, 16, 32)
+    assert not kernels.supported(q)
+    with pytest.raises(ValueError, match="CUDA"):
+        kernels.check_inputs(q, q, q)
+    with pytest.raises(ValueError, match="must all be"):
+        kernels.check_inputs(q, q[:, :, :8], q)
+    with pytest.raises(ValueError, match="dot_precision"):
+        kernels._resolve_precision("fp8", torch.float32)
+    assert kernels._resolve_precision(None, torch.bfloat16) == _lib.DTYPE_BF16
+    assert kernels._resolve_precision(None, torch.float16) == _lib.DTYPE_F32
+    with pytest.raises(ValueError, match="exempt"):
+        kernels._check_exempt(0)
+    with pytest.raises(ValueError, match="bwd_group"):
+        kernels._check_bwd_group(3)
+    with pytest.raises(ValueError, match="damp"):
+        kernels._damp_mode("cubic", 10)
+    with pytest.raises(ValueError, match="train_len"):
+        kernels._damp_mode("linear", 0)
+    with pytest.raises(ValueError, match="multiples"):
+        kernels._check_blocks(48, 32)
