@@ -90,15 +90,16 @@ int64_t sa_backward_workspace_bytes(int64_t nseq, int64_t heads, int64_t t, int6
  * _selective_backward[_pair] launch and the head-0 merge), reference
  * src/selective_attention/kernels.py:621-666. Inputs are those of a full forward
  * (q_offset 0, tq == tk == t) plus its out, rmax, rden and carry, and dout in the storage
- * dtype. dq, dk, dv receive the gradients in the storage dtype, head 0's selection path
- * included.
+ * dtype. dq, dk, dv receive the gradients, head 0's selection path included, in grad_dtype
+ * (SA_DTYPE_BF16 or SA_DTYPE_F32; the reference accumulates in fp32 and casts to the input
+ * dtype, kernels.py:664-666, so fp32 inputs run with bf16 operands get fp32 gradients).
  */
 int sa_backward(const void* q, const void* k, const void* v, const float* out, const void* dout,
                 const float* rmax, const float* rden, const float* carry,
                 void* dq, void* dk, void* dv,
                 void* workspace, int64_t workspace_bytes,
                 int64_t nseq, int64_t heads, int64_t t, int64_t head_dim, float scale, int dtype,
-                int exempt, int group, void* stream);
+                int grad_dtype, int exempt, int group, void* stream);
 
 #ifdef __cplusplus
 }

@@ -103,10 +103,23 @@ struct OpBF16 {
     for (int t = 0; t < 8; ++t) f[t] = (bf16_t)c[8 * s + t];
     return f;
   }
+  // The rounding residual of from_acc: c - bf16(c), itself rounded. hi + lo carries about 16
+  // significant bits, so a product taken on both keeps its sum close to fp32.
+  static constexpr bool SPLIT = true;
+  static __device__ __forceinline__ frag from_acc_lo(const f32x16& c, int s) {
+    frag f;
+#pragma unroll
+    for (int t = 0; t < 8; ++t) {
+      const float x = c[8 * s + t];
+      f[t] = (bf16_t)(x - (float)(bf16_t)x);
+    }
+    return f;
+  }
   static __device__ __forceinline__ elem to_elem(float x) {
     bf16_t b = (bf16_t)x;
     return *reinterpret_cast<elem*>(&b);
   }
+  static __device__ __forceinline__ elem to_elem_lo(float x) { return to_elem(x - to_float(to_elem(x))); }
   static __device__ __forceinline__ float to_float(elem x) {
     return __uint_as_float(((uint32_t)x) << 16);
   }
@@ -131,7 +144,10 @@ struct OpF32 {
     return p[r * ld + crow(s, h)];
   }
   static __device__ __forceinline__ frag from_acc(const f32x16& c, int s) { return c[s]; }
+  static constexpr bool SPLIT = false;   // fp32 operands are exact already
+  static __device__ __forceinline__ frag from_acc_lo(const f32x16& c, int s) { return 0.f; }
   static __device__ __forceinline__ elem to_elem(float x) { return x; }
+  static __device__ __forceinline__ elem to_elem_lo(float x) { return 0.f; }
   static __device__ __forceinline__ float to_float(elem x) { return x; }
   static constexpr int acc_steps = 16;
 };
@@ -603,24 +619,62 @@ __global__ __launch_bounds__(NTHREADS) void bwd_kernel(
   const float sl2 = scale * LOG2E;
   const int qb_lo = (blockIdx.x * NWAVES * TILE) / TILE;
 
-  // dz (C layout, queries x keys) -> LDS -> dQ tile += dz K -> atomics into dq rows of qb.
-  auto dq_update = [&](const f32x16& dzv, const frag (&ktfr)[DB][AS], float* dqh, int qb) {
+  // acc[db] (D x keys) += Y^T X: Y a staged [rows][D]^T LDS tile (rows d, queries in C-layout
+  // order), X a C-layout (queries x keys) tile. With split, X also enters as its rounding residual.
+  auto acc_t = [&](f32x16 (&acc)[DB], const elem* yt, const f32x16& x, bool split) {
+#pragma unroll
+    for (int db = 0; db < DB; ++db)
+#pragma unroll
+      for (int s = 0; s < AS; ++s) acc[db] = OP::mma(OP::ld_perm(yt, LDV, db * 32 + n, h, s), OP::from_acc(x, s), acc[db]);
+    if constexpr (OP::SPLIT) {
+      if (split) {
+#pragma unroll
+        for (int db = 0; db < DB; ++db)
+#pragma unroll
+          for (int s = 0; s < AS; ++s)
+            acc[db] = OP::mma(OP::ld_perm(yt, LDV, db * 32 + n, h, s), OP::from_acc_lo(x, s), acc[db]);
+      }
+    }
+  };
+
+  // dz (C layout, queries x keys) -> LDS -> dQ tile += dz K -> atomics into dq rows of qb. With
+  // split, the rounding residual of dz takes a second pass through LDS.
+  auto dq_update = [&](const f32x16& dzv, const frag (&ktfr)[DB][AS], float* dqh, int qb, bool split) {
+    f32x16 acc[DB];
+#pragma unroll
+    for (int db = 0; db < DB; ++db) acc[db] = zero16();
 #pragma unroll
     for (int i = 0; i < 16; ++i) zs[crow(i, h) * LDZ + n] = OP::to_elem(dzv[i]);
     lds_wave_sync();
 #pragma unroll
-    for (int db = 0; db < DB; ++db) {
-      f32x16 acc = zero16();
+    for (int db = 0; db < DB; ++db)
 #pragma unroll
-      for (int s = 0; s < AS; ++s) acc = OP::mma(OP::ld_std(zs, LDZ, n, h, s), ktfr[db][s], acc);
+      for (int s = 0; s < AS; ++s) acc[db] = OP::mma(OP::ld_std(zs, LDZ, n, h, s), ktfr[db][s], acc[db]);
+    if constexpr (OP::SPLIT) {
+      if (split) {
+        lds_wave_sync();
+#pragma unroll
+        for (int i = 0; i < 16; ++i) zs[crow(i, h) * LDZ + n] = OP::to_elem_lo(dzv[i]);
+        lds_wave_sync();
+#pragma unroll
+        for (int db = 0; db < DB; ++db)
+#pragma unroll
+          for (int s = 0; s < AS; ++s) acc[db] = OP::mma(OP::ld_std(zs, LDZ, n, h, s), ktfr[db][s], acc[db]);
+      }
+    }
+#pragma unroll
+    for (int db = 0; db < DB; ++db)
 #pragma unroll
       for (int i = 0; i < 16; ++i) {
         const int r = qb * TILE + crow(i, h);
-        if (r < T) atomicAdd(dqh + (int64_t)r * D + db * 32 + n, acc[i]);
+        if (r < T) atomicAdd(dqh + (int64_t)r * D + db * 32 + n, acc[db][i]);
       }
-    }
     lds_wave_sync();
   };
+
+  // Keys below `exempt` are never selected, so they gather attention from every later query and
+  // their dV / dK sums run over all of them: their products take the split operands.
+  const bool split_keys = key0 < exempt;
 
   for (int qb = NB - 1; qb >= qb_lo; --qb) {
     const int qbase = qb * TILE;
@@ -719,22 +773,14 @@ __global__ __launch_bounds__(NTHREADS) void bwd_kernel(
         }
       }
       // dV^T += dO^T P
-#pragma unroll
-      for (int db = 0; db < DB; ++db)
-#pragma unroll
-        for (int s = 0; s < AS; ++s)
-          dvt[g][db] = OP::mma(OP::ld_perm(sdOt[g], LDV, db * 32 + n, h, s), OP::from_acc(pr, s), dvt[g][db]);
+      acc_t(dvt[g], sdOt[g], pr, split_keys);
 #pragma unroll
       for (int i = 0; i < 16; ++i) dzsum[i] += dz[i];
       if (has_h0 && g == 0) {
         dz0 = dz;
       } else {
-#pragma unroll
-        for (int db = 0; db < DB; ++db)
-#pragma unroll
-          for (int s = 0; s < AS; ++s)
-            dkt[g][db] = OP::mma(OP::ld_perm(sQt[g], LDV, db * 32 + n, h, s), OP::from_acc(dz, s), dkt[g][db]);
-        dq_update(dz, ktf[g], dq + row * T * D, qb);
+        acc_t(dkt[g], sQt[g], dz, split_keys);
+        dq_update(dz, ktf[g], dq + row * T * D, qb, false);
       }
     }
 
@@ -763,23 +809,21 @@ __global__ __launch_bounds__(NTHREADS) void bwd_kernel(
       ucarry = run;
     }
 
+    // g sums dz over every later query of every head: it outgrows the dz tiles, so head 0's
+    // products take it split (the group holding head 0 always, the others when some |g| > 1/4).
     if (has_h0) {
       f32x16 dzh;
 #pragma unroll
       for (int i = 0; i < 16; ++i) dzh[i] = dz0[i] + gpath[i];
-#pragma unroll
-      for (int db = 0; db < DB; ++db)
-#pragma unroll
-        for (int s = 0; s < AS; ++s)
-          dkt[0][db] = OP::mma(OP::ld_perm(sQt[0], LDV, db * 32 + n, h, s), OP::from_acc(dzh, s), dkt[0][db]);
-      dq_update(dzh, ktf[0], dq + seq_row * T * D, qb);
+      acc_t(dkt[0], sQt[0], dzh, true);
+      dq_update(dzh, ktf[0], dq + seq_row * T * D, qb, true);
     } else {
+      bool big = false;
 #pragma unroll
-      for (int db = 0; db < DB; ++db)
-#pragma unroll
-        for (int s = 0; s < AS; ++s)
-          dk0t[db] = OP::mma(OP::ld_perm(sQt[G], LDV, db * 32 + n, h, s), OP::from_acc(gpath, s), dk0t[db]);
-      dq_update(gpath, k0tf, dq + seq_row * T * D, qb);
+      for (int i = 0; i < 16; ++i) big |= fabsf(gpath[i]) > 0.25f;
+      const bool split_g = __any(big);
+      acc_t(dk0t, sQt[G], gpath, split_g);
+      dq_update(gpath, k0tf, dq + seq_row * T * D, qb, split_g);
     }
   }
 
@@ -810,20 +854,23 @@ __global__ __launch_bounds__(NTHREADS) void bwd_kernel(
   }
 }
 
-// Gradients to the storage dtype: dq*scale, dk (+ head 0's share from other groups), dv.
-template <class OP>
+// Gradients to the output dtype (bf16 or fp32): dq*scale, dk (+ head 0's share from other groups), dv.
+__device__ __forceinline__ void store_grad(uint16_t* p, float x) { *p = OpBF16::to_elem(x); }
+__device__ __forceinline__ void store_grad(float* p, float x) { *p = x; }
+
+template <typename OUT>
 __global__ __launch_bounds__(NTHREADS) void bwd_finish_kernel(
     const float* __restrict__ dq32, const float* __restrict__ dk32, const float* __restrict__ dv32,
-    const float* __restrict__ dk0x, typename OP::elem* __restrict__ dq, typename OP::elem* __restrict__ dk,
-    typename OP::elem* __restrict__ dv, int H, int64_t TD, int64_t total, float scale) {
+    const float* __restrict__ dk0x, OUT* __restrict__ dq, OUT* __restrict__ dk, OUT* __restrict__ dv, int H,
+    int64_t TD, int64_t total, float scale) {
   for (int64_t e = (int64_t)blockIdx.x * NTHREADS + threadIdx.x; e < total; e += (int64_t)gridDim.x * NTHREADS) {
     const int64_t row = e / TD;          // b*H + head
     const int64_t off = e - row * TD;
     float kv = dk32[e];
     if (row % H == 0) kv += dk0x[(row / H) * TD + off];
-    dq[e] = OP::to_elem(dq32[e] * scale);
-    dk[e] = OP::to_elem(kv);
-    dv[e] = OP::to_elem(dv32[e]);
+    store_grad(dq + e, dq32[e] * scale);
+    store_grad(dk + e, kv);
+    store_grad(dv + e, dv32[e]);
   }
 }
 
@@ -940,7 +987,8 @@ void launch_bwd(const typename OP::elem* q, const typename OP::elem* k, const ty
 template <class OP, int D>
 int backward_impl(const void* q_, const void* k_, const void* v_, const float* out, const void* dout_,
                   const float* rmax, const float* rden, const float* carry, void* dq_, void* dk_, void* dv_,
-                  void* ws, int nseq, int H, int T, float scale, int exempt, int group, hipStream_t st) {
+                  void* ws, int nseq, int H, int T, float scale, int exempt, int group, int grad_dtype,
+                  hipStream_t st) {
   using elem = typename OP::elem;
   const elem* q = static_cast<const elem*>(q_);
   const elem* k = static_cast<const elem*>(k_);
@@ -979,9 +1027,15 @@ int backward_impl(const void* q_, const void* k_, const void* v_, const float* o
                          scale, st);
   }
   const int64_t total = R * T * D;
-  hipLaunchKernelGGL((bwd_finish_kernel<OP>), dim3((unsigned)std::min<int64_t>(cdiv(total, NTHREADS), 8192)),
-                     dim3(NTHREADS), 0, st, dq32, dk32, dv32, dk0x, static_cast<elem*>(dq_), static_cast<elem*>(dk_),
-                     static_cast<elem*>(dv_), H, (int64_t)T * D, total, scale);
+  const dim3 fgrid((unsigned)std::min<int64_t>(cdiv(total, NTHREADS), 8192));
+  if (grad_dtype == SA_DTYPE_F32)
+    hipLaunchKernelGGL((bwd_finish_kernel<float>), fgrid, dim3(NTHREADS), 0, st, dq32, dk32, dv32, dk0x,
+                       static_cast<float*>(dq_), static_cast<float*>(dk_), static_cast<float*>(dv_), H,
+                       (int64_t)T * D, total, scale);
+  else
+    hipLaunchKernelGGL((bwd_finish_kernel<uint16_t>), fgrid, dim3(NTHREADS), 0, st, dq32, dk32, dv32, dk0x,
+                       static_cast<uint16_t*>(dq_), static_cast<uint16_t*>(dk_), static_cast<uint16_t*>(dv_), H,
+                       (int64_t)T * D, total, scale);
   return launch_status();
 }
 
@@ -1057,19 +1111,20 @@ int64_t sa_backward_workspace_bytes(int64_t nseq, int64_t heads, int64_t t, int6
 int sa_backward(const void* q, const void* k, const void* v, const float* out, const void* dout, const float* rmax,
                 const float* rden, const float* carry, void* dq, void* dk, void* dv, void* workspace,
                 int64_t workspace_bytes, int64_t nseq, int64_t heads, int64_t t, int64_t head_dim, float scale,
-                int dtype, int exempt, int group, void* stream) {
+                int dtype, int grad_dtype, int exempt, int group, void* stream) {
   if (!valid_dims(nseq, heads, t) || exempt < 1) return SA_ERR_ARGUMENT;
   if (!(scale > 0.f) || !(scale < INFINITY)) return SA_ERR_ARGUMENT;
   if (!q || !k || !v || !out || !dout || !rmax || !rden || !carry || !dq || !dk || !dv || !workspace)
     return SA_ERR_ARGUMENT;
   if (dtype != SA_DTYPE_BF16 && dtype != SA_DTYPE_F32) return SA_ERR_DTYPE;
+  if (grad_dtype != SA_DTYPE_BF16 && grad_dtype != SA_DTYPE_F32) return SA_ERR_DTYPE;
   if (head_dim != 32 && head_dim != 64 && head_dim != 128) return SA_ERR_HEAD_DIM;
   if (workspace_bytes < sa_backward_workspace_bytes(nseq, heads, t, head_dim, dtype)) return SA_ERR_WORKSPACE;
   hipStream_t st = static_cast<hipStream_t>(stream);
   const int ns = (int)nseq, H = (int)heads, T = (int)t;
 #define SA_BWD(OPT, DD) \
   return backward_impl<OPT, DD>(q, k, v, out, dout, rmax, rden, carry, dq, dk, dv, workspace, ns, H, T, scale, exempt, \
-                                group, st)
+                                group, grad_dtype, st)
   if (dtype == SA_DTYPE_BF16) {
     if (head_dim == 32) SA_BWD(OpBF16, 32);
     if (head_dim == 64) SA_BWD(OpBF16, 64);

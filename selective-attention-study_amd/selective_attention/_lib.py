@@ -31,7 +31,7 @@ SIGNATURES = {
                         _I64, _I64, _I64, _I64, _I64, _I64, _F, _I, _I, _I, _I, _I64, _P]),
     "sa_backward_workspace_bytes": (_I64, [_I64, _I64, _I64, _I64, _I]),
     "sa_backward": (_I, [_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _I64,
-                         _I64, _I64, _I64, _I64, _F, _I, _I, _I, _P]),
+                         _I64, _I64, _I64, _I64, _F, _I, _I, _I, _I, _P]),
 }
 
 _lock = threading.Lock()

@@ -316,17 +316,21 @@ class _SelectiveAttentionFn(torch.autograd.Function):
         n, seq, kdim = qs.shape
         dev = qs.device
         dos = _storage(dout, n, dtype, kdim)
-        dq = torch.empty_like(qs)
-        dk = torch.empty_like(ks)
-        dv = torch.empty_like(vs)
+        # gradients leave the kernel in the input dtype when every input is stored as-is (bf16 inputs
+        # on bf16 operands); otherwise in fp32, cast below (the reference's dq.to(q.dtype))
+        as_bf16 = dtype == _lib.DTYPE_BF16 and all(d == torch.bfloat16 for d in dtypes)
+        gdt = torch.bfloat16 if as_bf16 else torch.float32
+        dq = torch.empty(qs.shape, device=dev, dtype=gdt)
+        dk = torch.empty(ks.shape, device=dev, dtype=gdt)
+        dv = torch.empty(vs.shape, device=dev, dtype=gdt)
         ws_bytes = lib.sa_backward_workspace_bytes(batch, heads, seq, kdim, dtype)
         ws = torch.empty(int(ws_bytes), device=dev, dtype=torch.uint8)
         with torch.cuda.device(dev):
             _lib.check(lib.sa_backward(
                 qs.data_ptr(), ks.data_ptr(), vs.data_ptr(), out.data_ptr(), dos.data_ptr(), rmax.data_ptr(),
                 rden.data_ptr(), carry.data_ptr(), dq.data_ptr(), dk.data_ptr(), dv.data_ptr(), ws.data_ptr(),
-                ws.numel(), batch, heads, seq, kdim, 1.0 / math.sqrt(head_dim), dtype, exempt, group,
-                _stream(dev)))
+                ws.numel(), batch, heads, seq, kdim, 1.0 / math.sqrt(head_dim), dtype,
+                _lib.DTYPE_BF16 if as_bf16 else _lib.DTYPE_F32, exempt, group, _stream(dev)))
         shape4 = (batch, heads, seq, head_dim)
         grads = tuple(g[..., :head_dim].reshape(shape4).to(want) for g, want in zip((dq, dk, dv), dtypes))
         return grads + (None,) * 11

@@ -69,13 +69,16 @@ def test_invalid_arguments_are_rejected_before_any_launch():
     bad = list(args)
     bad[20] = 0          # exempt
     assert lib.sa_forward(*bad) == -1
-    bargs = [fake] * 12 + [1 << 30, 1, 4, 16, 64, 0.125, 0, 1, 0, None]
+    bargs = [fake] * 12 + [1 << 30, 1, 4, 16, 64, 0.125, 0, 1, 1, 0, None]
     bad = list(bargs)
     bad[16] = 100
     assert lib.sa_backward(*bad) == -2
     bad = list(bargs)
     bad[17] = -1.0
     assert lib.sa_backward(*bad) == -1
+    bad = list(bargs)
+    bad[19] = 5          # grad dtype
+    assert lib.sa_backward(*bad) == -3
 
 
 def test_api_checks_on_cpu_tensors():

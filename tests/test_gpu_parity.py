@@ -294,20 +294,44 @@ def test_per_head_selection_matches_each_head_alone(cuda):
 
 # -- BASELINE configurations ---------------------------------------------------------------------------
 
-def test_c2_slice_bf16_within_2e_2(cuda):
-    """C2 parity: bf16 fwd+bwd at B=1, H=16, T=2048, D=64 against the fp64 oracle on the same
-    bf16-rounded inputs; max-abs 2e-2 on out, dq, dk, dv."""
+def _c2_slice_inputs():
     g = torch.Generator().manual_seed(1234)
-    q, k, v, do = (torch.randn(1, 16, 2048, 64, generator=g).bfloat16() for _ in range(4))
-    qq, kk, vv = (t.to(cuda).requires_grad_(True) for t in (q, k, v))
-    out = kernels.selective_attention(qq, kk, vv)
+    return tuple(torch.randn(1, 16, 2048, 64, generator=g).bfloat16() for _ in range(4))
+
+
+def test_c2_slice_bf16_within_2e_2(cuda):
+    """C2 parity: bf16-operand fwd+bwd at B=1, H=16, T=2048, D=64 against the fp64 oracle on the same
+    bf16-valued inputs; max-abs 2e-2 on out, dq, dk, dv. The inputs are fp32 tensors holding bf16
+    values with dot_precision="bf16": the kernels run exactly the bf16 MFMA path and return the fp32
+    gradient accumulators (gradients follow the input dtype, as in the reference)."""
+    q, k, v, do = _c2_slice_inputs()
+    qq, kk, vv = (t.float().to(cuda).requires_grad_(True) for t in (q, k, v))
+    out = kernels.selective_attention(qq, kk, vv, dot_precision="bf16")
     out.backward(do.to(cuda).float())
+    assert qq.grad.dtype == torch.float32
     want, wgrads = _oracle_fwd_bwd(q, k, v, do.float())
     errs = {"out": (out.detach().cpu().double() - want).abs().max().item()}
     for name, gr, wg in zip(("dq", "dk", "dv"), (qq.grad, kk.grad, vv.grad), wgrads):
         errs[name] = (gr.cpu().double() - wg).abs().max().item()
     print("C2 slice max-abs errors:", errs, flush=True)
     assert all(e < 2e-2 for e in errs.values()), errs
+
+
+def test_c2_slice_bf16_inputs_bf16_gradients(cuda):
+    """The same slice with bf16 tensors: gradients come back in bf16, so each element also carries
+    the rounding of its own bf16 representation (half an ulp: up to 0.0625 at |g| in [16, 32))."""
+    q, k, v, do = _c2_slice_inputs()
+    qq, kk, vv = (t.to(cuda).requires_grad_(True) for t in (q, k, v))
+    out = kernels.selective_attention(qq, kk, vv)
+    out.backward(do.to(cuda).float())
+    want, wgrads = _oracle_fwd_bwd(q, k, v, do.float())
+    assert (out.detach().cpu().double() - want).abs().max().item() < 2e-2
+    for name, gr, wg in zip(("dq", "dk", "dv"), (qq.grad, kk.grad, vv.grad), wgrads):
+        assert gr.dtype == torch.bfloat16
+        wb = wg.to(torch.bfloat16).double()
+        half_ulp = (wb.abs() * 2.0 ** -8).clamp(min=2.0 ** -133)
+        excess = ((gr.cpu().double() - wg).abs() - half_ulp).max().item()
+        assert excess < 2e-2, (name, excess)
 
 
 def test_c2_full_length_prefix_is_exact(cuda):
