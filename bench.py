@@ -1,0 +1,170 @@
+"""Benchmark of the Selective Attention operator on one MI355X.
+
+One step = one fused forward + backward of the operator through the reference's API
+(`selective_attention(q, k, v)` then the gradients of q, k, v for an upstream gradient dO) at
+B=1, H=16, T=16384, D=64 in bf16, inputs already resident in HBM. The step includes everything
+the autograd op launches: the selection scan, the forward, the backward's transposes / row
+statistics / zeroing, the backward kernel and the gradient epilogue.
+
+Printed (rank 0, one JSON line): TFLOP/s under the FlashAttention convention (forward 2*B*H*D*T^2,
+forward + backward 7*B*H*D*T^2, causal pairs counted as T^2/2), the roofline of the dominant kernel
+(the backward kernel: algorithmic FLOP per launch / its average HIP-event duration inside the timed
+region, against the 2.5 PFLOP/s dense bf16 MFMA peak), and a CPU baseline: the fp32 listing (the
+test oracle) timed on this host for a bounded sample of the same workload.
+
+    python bench.py [--steps K] [--warmup W] [--no-cpu-baseline]
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import platform
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+for _p in (os.path.join(ROOT, "selective-attention-study_amd"), ROOT):
+    if _p not in sys.path:
+        sys.path.insert(0, _p)
+
+B, H, T, D = 1, 16, 16384, 64
+PEAK_BF16_TFLOPS = 2500.0          # MI355X dense bf16 MFMA, published
+FWD_FLOP = 2.0 * B * H * D * T * T
+BWD_FLOP = 5.0 * B * H * D * T * T
+STEP_FLOP = FWD_FLOP + BWD_FLOP    # 7 * B * H * D * T^2 = 1.9241e12
+
+
+def _cpu_model() -> str:
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return platform.processor() or "unknown"
+
+
+def cpu_baseline(budget_s: float = 20.0) -> dict:
+    """The fp32 listing (oracle/sa_oracle.py) forward + autograd backward on the host CPU, on the C2
+    parity slice B=1, H=16, T=2048, D=64: one warm-up, then repetitions until about budget_s."""
+
+    import torch
+
+    from oracle import sa_oracle
+
+    t = 2048
+    g = torch.Generator().manual_seed(0)
+    q, k, v, do = (torch.randn(B, H, t, D, generator=g) for _ in range(4))
+    q.requires_grad_(True), k.requires_grad_(True), v.requires_grad_(True)
+
+    def run():
+        out = sa_oracle.attention(q, k, v)
+        torch.autograd.grad(out, (q, k, v), do)
+
+    run()
+    times = []
+    t_end = time.perf_counter() + budget_s
+    while time.perf_counter() < t_end or len(times) < 3:
+        t0 = time.perf_counter()
+        run()
+        times.append(time.perf_counter() - t0)
+    times.sort()
+    med = times[len(times) // 2]
+    flop = 7.0 * B * H * D * t * t
+    return {
+        "value": flop / med / 1e12,
+        "unit": "TFLOP/s",
+        "cores": torch.get_num_threads(),
+        "kind": "port",
+        "sample": (f"fp32 listing (oracle/sa_oracle.py, torch on CPU) fwd+bwd at B=1 H=16 T=2048 D=64, "
+                   f"median of {len(times)} reps = {med * 1e3:.0f} ms; 7*B*H*D*T^2 FLOP; "
+                   f"{len(os.sched_getaffinity(0))} cores visible, CPU {_cpu_model()}"),
+    }
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print("bench.py measures one GPU only: the operator runs on a single MI355X "
+              "(multi-GPU sharding is described in DESIGN.md, not run)", file=sys.stderr)
+        return 2
+
+    import torch
+
+    from selective_attention import _lib, kernels
+
+    if not torch.cuda.is_available():
+        print("bench.py needs a ROCm GPU", file=sys.stderr)
+        return 2
+    if not kernels.HAS_HIP:
+        _lib.load()   # raises with the reason
+    dev = torch.device("cuda:0")
+    g = torch.Generator(device=dev).manual_seed(0)
+    q, k, v = (torch.randn(B, H, T, D, device=dev, generator=g).bfloat16().requires_grad_(True) for _ in range(3))
+    do = torch.randn(B, H, T, D, device=dev, generator=g)
+
+    def step():
+        out = kernels.selective_attention(q, k, v)
+        return torch.autograd.grad(out, (q, k, v), do)
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+
+    _lib.timing_enable(True)
+    start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    start.record()
+    for _ in range(args.steps):
+        grads = step()
+    stop.record()
+    torch.cuda.synchronize()
+    ms = start.elapsed_time(stop) / args.steps
+    per_kernel = {}
+    for name, kid in (("forward", _lib.KERNEL_FORWARD), ("backward", _lib.KERNEL_BACKWARD),
+                      ("selection", _lib.KERNEL_SELECTION)):
+        total, n = _lib.timing_read(kid)
+        per_kernel[name] = total / max(n, 1)
+    _lib.timing_enable(False)
+    assert all(torch.isfinite(gr).all().item() for gr in grads)
+
+    tflops = STEP_FLOP / (ms * 1e-3) / 1e12
+    bwd_ms = per_kernel["backward"]
+    achieved = BWD_FLOP / (bwd_ms * 1e-3) / 1e12
+    record = {
+        "metric": "fused fwd+bwd TFLOP/s & MFMA util at T=16K H=16 D=64 bf16; train tok/s",
+        "value": round(tflops, 2),
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic: q, k, v, dO ~ N(0,1), fixed seed",
+        "config": {"workload": "C2: selective attention fused fwd+bwd, B=1 H=16 T=16384 D=64, exempt=1 (BOS)",
+                   "flop_per_step": STEP_FLOP, "flop_convention": "7*B*H*D*T^2 (fwd 2, bwd 5; causal T^2/2)"},
+        "frac_of_peak": round(tflops / PEAK_BF16_TFLOPS, 4),
+        "kernel_ms": {k_: round(v_, 4) for k_, v_ in per_kernel.items()},
+        "roofline": {"bound": "mfma", "kernel": "bwd_kernel (backward, 5*B*H*D*T^2 FLOP per launch)",
+                     "achieved": round(achieved, 2), "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
+                     "frac": round(achieved / PEAK_BF16_TFLOPS, 4), "traffic": None},
+    }
+    if not args.no_cpu_baseline:
+        record["cpu_baseline"] = cpu_baseline()
+    print(json.dumps(record), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -52,6 +52,22 @@ int sa_abi_version(void);
 /* Human-readable text for a status code (static storage). */
 const char* sa_status_string(int status);
 
+/*
+ * Kernel timing for measurement tools; no counterpart in the reference (which times whole calls
+ * with perf_counter, scripts/bench_kernels.py:36-58). While enabled, sa_forward and sa_backward
+ * record a pair of HIP events on their stream around each of their main kernels.
+ * sa_timing_enable(on) discards what was recorded and switches recording on (1) or off (0).
+ * sa_timing_read waits for the recorded events of one kernel and returns the summed duration in
+ * milliseconds and the number of launches. Not meant for production paths: the events cost a
+ * little time per launch.
+ */
+#define SA_KERNEL_FORWARD 0     /* the attention forward kernel */
+#define SA_KERNEL_BACKWARD 1    /* the key-parallel backward kernel */
+#define SA_KERNEL_SELECTION 2   /* head 0's selection column sums + scan */
+#define SA_KERNEL_COUNT 3
+int sa_timing_enable(int on);
+int sa_timing_read(int kernel, double* total_ms, int64_t* launches);
+
 /* Leading dimension (elements) of the transposed copies held in the workspaces. */
 int64_t sa_transposed_ld(int64_t t);
 

@@ -33,6 +33,9 @@
 #include <stdint.h>
 #include <math.h>
 #include <algorithm>
+#include <mutex>
+#include <utility>
+#include <vector>
 
 #include "sa.h"
 
@@ -877,6 +880,47 @@ __global__ __launch_bounds__(NTHREADS) void bwd_finish_kernel(
 // ---------------------------------------------------------------------------------------------
 // Host side.
 
+// Event timing of the main kernels, for measurement tools (sa_timing_enable / sa_timing_read).
+// Off by default; when on, each timed launch is bracketed by a pair of HIP events recorded on the
+// launch's own stream. The registry is the only mutable host state of the library.
+struct TimingRegistry {
+  std::mutex mu;
+  bool on = false;
+  std::vector<std::pair<hipEvent_t, hipEvent_t>> events[SA_KERNEL_COUNT];
+};
+TimingRegistry& timing() {
+  static TimingRegistry r;
+  return r;
+}
+
+// Brackets one launch: construct before it, destroy after it (both on stream st).
+class TimedLaunch {
+ public:
+  TimedLaunch(int kernel, hipStream_t st) : kernel_(kernel), st_(st) {
+    TimingRegistry& r = timing();
+    std::lock_guard<std::mutex> lock(r.mu);
+    if (!r.on) return;
+    if (hipEventCreate(&start_) != hipSuccess) return;
+    if (hipEventCreate(&stop_) != hipSuccess) {
+      (void)hipEventDestroy(start_);
+      return;
+    }
+    active_ = hipEventRecord(start_, st_) == hipSuccess;
+  }
+  ~TimedLaunch() {
+    if (!active_) return;
+    TimingRegistry& r = timing();
+    std::lock_guard<std::mutex> lock(r.mu);
+    if (hipEventRecord(stop_, st_) == hipSuccess) r.events[kernel_].emplace_back(start_, stop_);
+  }
+
+ private:
+  int kernel_;
+  hipStream_t st_;
+  hipEvent_t start_ = nullptr, stop_ = nullptr;
+  bool active_ = false;
+};
+
 inline int64_t align_up(int64_t x, int64_t a) { return (x + a - 1) / a * a; }
 inline int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
 
@@ -903,6 +947,7 @@ int run_selection(const typename OP::elem* q, const typename OP::elem* k, float*
   const int NBq = (int)cdiv(Tq, TILE), NKT = (int)cdiv(Tk, TILE);
   const int RB = 8;
   dim3 g1((unsigned)cdiv(NKT, NWAVES), (unsigned)cdiv(NBq, RB), (unsigned)nseq);
+  TimedLaunch timed(SA_KERNEL_SELECTION, st);
   hipLaunchKernelGGL((sel_colsum_kernel<OP, D>), g1, dim3(NTHREADS), 0, st, q, k, carry, H, Tq, Tk, q_off, exempt,
                      scale, RB);
   dim3 g2((unsigned)cdiv(Tk, NTHREADS), (unsigned)nseq);
@@ -917,6 +962,7 @@ void launch_fwd(const typename OP::elem* q, const typename OP::elem* k, const ty
                 int q_off, int64_t ldv, int exempt, float scale, int damp_mode, float train_len, hipStream_t st) {
   const int NBq = (int)cdiv(Tq, TILE);
   dim3 grid((unsigned)cdiv(NBq, NWAVES), (unsigned)(nseq * (H / G)));
+  TimedLaunch timed(SA_KERNEL_FORWARD, st);
   hipLaunchKernelGGL((fwd_kernel<OP, D, G>), grid, dim3(NTHREADS), 0, st, q, k, vt, carry, out, rmax, rden, H, Tq,
                      Tk, q_off, ldv, exempt, scale, damp_mode, train_len);
 }
@@ -980,6 +1026,7 @@ void launch_bwd(const typename OP::elem* q, const typename OP::elem* k, const ty
                 const float* lse, const float* dbar, const float* carry, float* dq, float* dk, float* dv,
                 float* dk0x, int nseq, int H, int T, int64_t ldt, int exempt, float scale, hipStream_t st) {
   dim3 grid((unsigned)cdiv(T, NWAVES * TILE), (unsigned)(nseq * (H / G)));
+  TimedLaunch timed(SA_KERNEL_BACKWARD, st);
   hipLaunchKernelGGL((bwd_kernel<OP, D, G>), grid, dim3(NTHREADS), 0, st, q, k, v, qt, dout, dot, lse, dbar, carry,
                      dq, dk, dv, dk0x, H, T, ldt, exempt, scale);
 }
@@ -1051,7 +1098,37 @@ bool valid_dims(int64_t nseq, int64_t heads, int64_t t) {
 
 extern "C" {
 
-int sa_abi_version(void) { return 1; }
+int sa_abi_version(void) { return 2; }
+
+int sa_timing_enable(int on) {
+  TimingRegistry& r = timing();
+  std::lock_guard<std::mutex> lock(r.mu);
+  for (auto& list : r.events) {
+    for (auto& ev : list) {
+      (void)hipEventDestroy(ev.first);
+      (void)hipEventDestroy(ev.second);
+    }
+    list.clear();
+  }
+  r.on = on != 0;
+  return SA_OK;
+}
+
+int sa_timing_read(int kernel, double* total_ms, int64_t* launches) {
+  if (kernel < 0 || kernel >= SA_KERNEL_COUNT || !total_ms || !launches) return SA_ERR_ARGUMENT;
+  TimingRegistry& r = timing();
+  std::lock_guard<std::mutex> lock(r.mu);
+  double sum = 0.0;
+  for (auto& ev : r.events[kernel]) {
+    float ms = 0.f;
+    if (hipEventSynchronize(ev.second) != hipSuccess || hipEventElapsedTime(&ms, ev.first, ev.second) != hipSuccess)
+      return SA_ERR_LAUNCH;
+    sum += ms;
+  }
+  *total_ms = sum;
+  *launches = (int64_t)r.events[kernel].size();
+  return SA_OK;
+}
 
 const char* sa_status_string(int status) {
   switch (status) {

@@ -17,6 +17,11 @@ LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), LIB_NAME)
 DTYPE_BF16 = 0
 DTYPE_F32 = 1
 
+# Kernel ids of sa_timing_read.
+KERNEL_FORWARD = 0
+KERNEL_BACKWARD = 1
+KERNEL_SELECTION = 2
+
 # Every function the header declares, with its ctypes signature.
 _P = ctypes.c_void_p
 _I64 = ctypes.c_int64
@@ -26,6 +31,8 @@ SIGNATURES = {
     "sa_abi_version": (_I, []),
     "sa_status_string": (ctypes.c_char_p, [_I]),
     "sa_transposed_ld": (_I64, [_I64]),
+    "sa_timing_enable": (_I, [_I]),
+    "sa_timing_read": (_I, [_I, ctypes.POINTER(ctypes.c_double), ctypes.POINTER(_I64)]),
     "sa_forward_workspace_bytes": (_I64, [_I64, _I64, _I64, _I64, _I]),
     "sa_forward": (_I, [_P, _P, _P, _P, _P, _P, _P, _P, _P, _I64, _P, _I64,
                         _I64, _I64, _I64, _I64, _I64, _I64, _F, _I, _I, _I, _I, _I64, _P]),
@@ -80,3 +87,18 @@ def check(status: int) -> None:
         lib = load()
         raise RuntimeError(f"selective attention HIP call failed ({status}): "
                            f"{lib.sa_status_string(status).decode()}")
+
+
+def timing_enable(on: bool) -> None:
+    """Discard recorded kernel timings and switch event recording on or off."""
+
+    check(load().sa_timing_enable(1 if on else 0))
+
+
+def timing_read(kernel: int) -> tuple[float, int]:
+    """(summed milliseconds, launches) recorded for one kernel id since timing_enable."""
+
+    total = ctypes.c_double(0.0)
+    count = ctypes.c_int64(0)
+    check(load().sa_timing_read(kernel, ctypes.byref(total), ctypes.byref(count)))
+    return total.value, count.value
