@@ -62,9 +62,10 @@ const char* sa_status_string(int status);
  * little time per launch.
  */
 #define SA_KERNEL_FORWARD 0     /* the attention forward kernel */
-#define SA_KERNEL_BACKWARD 1    /* the key-parallel backward kernel */
+#define SA_KERNEL_BACKWARD 1    /* the key-parallel backward kernel (dK, dV) */
 #define SA_KERNEL_SELECTION 2   /* head 0's selection column sums + scan */
-#define SA_KERNEL_COUNT 3
+#define SA_KERNEL_BACKWARD_DQ 3 /* the query-parallel backward kernel (dQ) */
+#define SA_KERNEL_COUNT 4
 int sa_timing_enable(int on);
 int sa_timing_read(int kernel, double* total_ms, int64_t* launches);
 
@@ -98,8 +99,8 @@ int sa_forward(const void* q, const void* k, const void* v,
                int64_t head_dim, float scale, int dtype, int exempt, int group,
                int damp_mode, int64_t train_len, void* stream);
 
-/* Bytes of scratch sa_backward needs. */
-int64_t sa_backward_workspace_bytes(int64_t nseq, int64_t heads, int64_t t, int64_t head_dim, int dtype);
+/* Bytes of scratch sa_backward needs for the same `group` argument (-1 for invalid sizes). */
+int64_t sa_backward_workspace_bytes(int64_t nseq, int64_t heads, int64_t t, int64_t head_dim, int dtype, int group);
 
 /*
  * Full backward pass: replaces _SelectiveAttentionFn.backward (dbar, zeroing, the
@@ -109,6 +110,9 @@ int64_t sa_backward_workspace_bytes(int64_t nseq, int64_t heads, int64_t t, int6
  * dtype. dq, dk, dv receive the gradients, head 0's selection path included, in grad_dtype
  * (SA_DTYPE_BF16 or SA_DTYPE_F32; the reference accumulates in fp32 and casts to the input
  * dtype, kernels.py:664-666, so fp32 inputs run with bf16 operands get fp32 gradients).
+ * group: heads per wavefront of the backward kernels (0 = automatic); the workspace size depends
+ * on it. Two kernels replace the reference's one: a key-parallel pass (dK, dV) and a
+ * query-parallel pass (dQ), so no gradient element is accumulated with per-tile atomics.
  */
 int sa_backward(const void* q, const void* k, const void* v, const float* out, const void* dout,
                 const float* rmax, const float* rden, const float* carry,

@@ -232,6 +232,82 @@ __device__ __forceinline__ void stage_cols(E* s, const E* g, int64_t gld, int co
   }
 }
 
+// Register-staged tiles for software pipelining: load() issues a tile's global loads into registers
+// (each thread owns PER 16-byte chunks), store() later writes them to LDS, so the loads of the next
+// tile are in flight while the current one is computed.
+
+// [32 rows][COLS] of a row-major global matrix (row stride gld); rows >= nrows read as zero. The
+// row index is clamped and the value zeroed by select, so the load has no branch.
+template <typename E, int COLS>
+struct RowTile {
+  static constexpr int EPC = 16 / sizeof(E);
+  static constexpr int CPR = COLS / EPC;
+  static constexpr int NCH = TILE * CPR;
+  static constexpr int PER = (NCH + NTHREADS - 1) / NTHREADS;
+  uint4 v[PER];
+  __device__ __forceinline__ void load(const E* g, int64_t gld, int row0, int nrows, int tid) {
+#pragma unroll
+    for (int p = 0; p < PER; ++p) {
+      const int c = (tid + p * NTHREADS) % NCH;   // PER * NTHREADS > NCH only for small tiles
+      const int r = c / CPR, cc = (c % CPR) * EPC;
+      const int rr = min(row0 + r, nrows - 1);
+      const uint4 x = *reinterpret_cast<const uint4*>(g + (int64_t)rr * gld + cc);
+      const bool ok = row0 + r < nrows;
+      v[p] = make_uint4(ok ? x.x : 0u, ok ? x.y : 0u, ok ? x.z : 0u, ok ? x.w : 0u);
+    }
+  }
+  template <int SLD>
+  __device__ __forceinline__ void store(E* s, int tid) const {
+    static_assert((SLD * sizeof(E)) % 16 == 0, "row stride must keep 16-byte alignment");
+#pragma unroll
+    for (int p = 0; p < PER; ++p) {
+      const int c = tid + p * NTHREADS;
+      const int r = (c % NCH) / CPR, cc = (c % CPR) * EPC;
+      if (NCH % NTHREADS == 0 || c < NCH) *reinterpret_cast<uint4*>(s + r * SLD + cc) = v[p];
+    }
+  }
+};
+
+// Columns col0..col0+31 of ROWS rows of one of this library's transposed copies: row stride gld,
+// a multiple of 64 elements, zero-filled past the sequence, so every 16-byte chunk is in bounds and
+// the load needs no check.
+template <typename E, int ROWS>
+struct ColTile {
+  static constexpr int EPC = 16 / sizeof(E);
+  static constexpr int CPR = TILE / EPC;
+  static constexpr int NCH = ROWS * CPR;
+  static constexpr int PER = (NCH + NTHREADS - 1) / NTHREADS;
+  uint4 v[PER];
+  __device__ __forceinline__ void load(const E* g, int64_t gld, int col0, int tid) {
+#pragma unroll
+    for (int p = 0; p < PER; ++p) {
+      const int c = (tid + p * NTHREADS) % NCH;
+      const int r = c / CPR, cc = (c % CPR) * EPC;
+      v[p] = *reinterpret_cast<const uint4*>(g + (int64_t)r * gld + col0 + cc);
+    }
+  }
+  template <int SLD>
+  __device__ __forceinline__ void store(E* s, int tid) const {
+#pragma unroll
+    for (int p = 0; p < PER; ++p) {
+      const int c = tid + p * NTHREADS;
+      const int r = (c % NCH) / CPR, cc = (c % CPR) * EPC;
+      if (!(NCH % NTHREADS == 0 || c < NCH)) continue;
+      E* dst = s + r * SLD + cc;
+      if constexpr (sizeof(E) == 2) {
+        static_assert((SLD * 2) % 8 == 0, "bf16 column tiles need 8-byte row alignment");
+        reinterpret_cast<uint2*>(dst)[0] = make_uint2(v[p].x, v[p].y);
+        reinterpret_cast<uint2*>(dst)[1] = make_uint2(v[p].z, v[p].w);
+      } else {
+        union { uint4 q; E e[EPC]; } u;
+        u.q = v[p];
+#pragma unroll
+        for (int e = 0; e < EPC; ++e) dst[e] = u.e[e];
+      }
+    }
+  }
+};
+
 // ---------------------------------------------------------------------------------------------
 // Lane scans (DPP) across the 32 lanes of each half-wavefront.
 
@@ -539,34 +615,136 @@ __global__ __launch_bounds__(NTHREADS) void fill_zero_kernel(float4* __restrict_
 }
 
 // ---------------------------------------------------------------------------------------------
-// Backward main kernel. grid (ceil(T/128), nseq * H/G); wavefront w owns keys
-// [x*128 + 32w, +32) of heads [gi*G, gi*G+G).
+// Backward kernel shape. SA_BWD_PIPE 1: the next tile's global loads are issued before the current
+// tile is computed (double-buffered LDS when it fits); 0: load, store, compute in turn, leaving the
+// overlap to a second workgroup on the CU. SA_BWD_MIN_BLOCKS: workgroups per CU the register
+// allocation must allow.
+#ifndef SA_BWD_PIPE
+#define SA_BWD_PIPE 1
+#endif
+#ifndef SA_BWD_MIN_BLOCKS
+#define SA_BWD_MIN_BLOCKS 1
+#endif
+constexpr bool BWD_PIPE = SA_BWD_PIPE != 0;
+
+// ---------------------------------------------------------------------------------------------
+// Backward helpers on (queries x keys) C-layout tiles: lane n holds key j = key0 + n, rows are the
+// queries qbase + crow(i, h), i = 0..15 (h = lane / 32).
+
+// Head 0's selection on a tile of its raw logits l0: S = relu(s l0) where exempt <= j < r < T,
+// the gate bits, and the history F[r, j] = hist_in + sum of S over the tile's earlier rows, in
+// log2 units (the running sum runs down the rows; the two half-wavefronts swap partial sums).
+// `edge` (wave-uniform) marks tiles where some pair fails exempt <= j < r < T; elsewhere the gate
+// is the sign of the logit alone.
+__device__ __forceinline__ void selection_tile(const f32x16& l0, float hist_in, int qbase, int j, int T,
+                                               int exempt, float scale, int h, bool edge, f32x16& fs,
+                                               uint32_t& gmask) {
+  f32x16 sel;
+  gmask = 0;
+  if (edge) {
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      const int r = qbase + crow(i, h);
+      const float sv = l0[i] * scale;
+      const bool gate = (r < T) && (j >= exempt) && (j < r) && (sv > 0.f);
+      sel[i] = gate ? sv : 0.f;
+      gmask |= gate ? (1u << i) : 0u;
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      const float sv = l0[i] * scale;
+      sel[i] = fmaxf(sv, 0.f);
+      gmask |= sv > 0.f ? (1u << i) : 0u;
+    }
+  }
+  float gs[4], pg[4];
+#pragma unroll
+  for (int a = 0; a < 4; ++a) gs[a] = ((sel[4 * a] + sel[4 * a + 1]) + sel[4 * a + 2]) + sel[4 * a + 3];
+#pragma unroll
+  for (int a = 0; a < 4; ++a) pg[a] = xor32(gs[a]);
+  float run = hist_in;
+#pragma unroll
+  for (int a = 0; a < 4; ++a) {
+    const float g_lo = h == 0 ? gs[a] : pg[a];   // rows 8a..8a+3
+    const float g_hi = h == 0 ? pg[a] : gs[a];   // rows 8a+4..8a+7
+    float p = (h == 0) ? run : run + g_lo;
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+      fs[4 * a + t] = p * LOG2E;
+      p += sel[4 * a + t];
+    }
+    run = (run + g_lo) + g_hi;
+  }
+}
+
+// Selection gradient path: U[r, j] = u_in + sum of z over the tile's later rows, and
+// g = -gate * U. Returns u_in + the sum over the whole tile (U entering the tile above).
+__device__ __forceinline__ float gpath_tile(const f32x16& z, float u_in, uint32_t gmask, int h, f32x16& gp) {
+  float gs[4], pg[4];
+#pragma unroll
+  for (int a = 0; a < 4; ++a) gs[a] = ((z[4 * a + 3] + z[4 * a + 2]) + z[4 * a + 1]) + z[4 * a];
+#pragma unroll
+  for (int a = 0; a < 4; ++a) pg[a] = xor32(gs[a]);
+  float run = u_in;
+#pragma unroll
+  for (int a = 3; a >= 0; --a) {
+    const float g_lo = h == 0 ? gs[a] : pg[a];
+    const float g_hi = h == 0 ? pg[a] : gs[a];
+    float p = (h == 1) ? run : run + g_hi;
+#pragma unroll
+    for (int t = 3; t >= 0; --t) {
+      const int i = 4 * a + t;
+      gp[i] = ((gmask >> i) & 1u) ? -p : 0.f;
+      p += z[i];
+    }
+    run = (run + g_hi) + g_lo;
+  }
+  return run;
+}
+
+// Whether some |g| of the wavefront's tile is large enough for the split-operand products: g sums
+// dz over every later query of the group's heads and can outgrow the dz tiles many times.
+__device__ __forceinline__ bool big_tile(const f32x16& x) {
+  bool big = false;
+#pragma unroll
+  for (int i = 0; i < 16; ++i) big |= fabsf(x[i]) > 0.25f;
+  return __any(big);
+}
+
+// ---------------------------------------------------------------------------------------------
+// Backward, key side. grid (ceil(T/128), nseq * H/G); wavefront w owns keys [x*128 + 32w, +32) of
+// heads [gi*G, gi*G+G) and sweeps the query tiles last to first, with K, V and the dK, dV sums in
+// registers. The selection suffix U (over this group's heads) is checkpointed on entry to every
+// query tile into ucheck[gi][b][qb][j] for the dQ kernel. Head 0's dK gets g = -gate*U from every
+// group: the group holding head 0 folds it into head 0's dz; the others add their share to dk0x.
 
 template <class OP, int D, int G>
-__global__ __launch_bounds__(NTHREADS) void bwd_kernel(
+__global__ __launch_bounds__(NTHREADS, SA_BWD_MIN_BLOCKS) void bwd_kv_kernel(
     const typename OP::elem* __restrict__ q, const typename OP::elem* __restrict__ k,
     const typename OP::elem* __restrict__ v, const typename OP::elem* __restrict__ qt,
     const typename OP::elem* __restrict__ dout, const typename OP::elem* __restrict__ dot,
     const float* __restrict__ lse, const float* __restrict__ dbar, const float* __restrict__ carry,
-    float* __restrict__ dq, float* __restrict__ dk, float* __restrict__ dv, float* __restrict__ dk0x,
-    int H, int T, int64_t ldt, int exempt, float scale) {
+    float* __restrict__ ucheck, float* __restrict__ dk, float* __restrict__ dv, float* __restrict__ dk0x,
+    int nseq, int H, int T, int64_t ldt, int exempt, float scale) {
   using elem = typename OP::elem;
   using frag = typename OP::frag;
   constexpr int NS = D / OP::KS;
   constexpr int DB = D / 32;
   constexpr int LDK = D + OP::KPAD;
   constexpr int LDV = TILE + OP::TPAD;
-  constexpr int LDZ = TILE + OP::KPAD;
   constexpr int AS = OP::acc_steps;
   constexpr int NH = G + 1;   // staged heads: the group, then head 0 when outside the group
+  // two buffers (the tile being computed, the next one being written) when they fit in LDS
+  constexpr int TILE_BYTES = (NH * (TILE * LDK + D * LDV) + G * (TILE * LDK + D * LDV)) * (int)sizeof(elem);
+  constexpr int NBUF = (BWD_PIPE && 2 * TILE_BYTES <= 120 * 1024) ? 2 : 1;
 
-  __shared__ __attribute__((aligned(16))) elem sQ[NH][TILE * LDK];
-  __shared__ __attribute__((aligned(16))) elem sQt[NH][D * LDV];
-  __shared__ __attribute__((aligned(16))) elem sdO[G][TILE * LDK];
-  __shared__ __attribute__((aligned(16))) elem sdOt[G][D * LDV];
-  __shared__ __attribute__((aligned(16))) float sLse[G][TILE];
-  __shared__ __attribute__((aligned(16))) float sDb[G][TILE];
-  __shared__ __attribute__((aligned(16))) elem sZ[NWAVES][TILE * LDZ];
+  __shared__ __attribute__((aligned(16))) elem sQ[NBUF][NH][TILE * LDK];
+  __shared__ __attribute__((aligned(16))) elem sQt[NBUF][NH][D * LDV];
+  __shared__ __attribute__((aligned(16))) elem sdO[NBUF][G][TILE * LDK];
+  __shared__ __attribute__((aligned(16))) elem sdOt[NBUF][G][D * LDV];
+  __shared__ __attribute__((aligned(16))) float sLse[NBUF][G][TILE];
+  __shared__ __attribute__((aligned(16))) float sDb[NBUF][G][TILE];
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int n = lane & 31, h = lane >> 5;
@@ -578,11 +756,11 @@ __global__ __launch_bounds__(NTHREADS) void bwd_kernel(
   const int key0 = blockIdx.x * (NWAVES * TILE) + wave * TILE;
   const int j = key0 + n;
   const int64_t seq_row = (int64_t)b * H;
-  elem* zs = sZ[wave];
+  float* uplane = ucheck + ((int64_t)gi * nseq + b) * NB * (int64_t)T;
+  const float* carry_col = carry + (int64_t)b * NB * T + (j < T ? j : 0);
 
-  // Key-side operands in registers.
-  frag kf[G][NS], vf[G][NS], ktf[G][DB][AS];
-  frag k0f[NS], k0tf[DB][AS];
+  // Key-side operands in registers (B operands: lane = key column).
+  frag kf[G][NS], vf[G][NS], k0f[NS];
 #pragma unroll
   for (int g = 0; g < G; ++g) {
     const elem* kh = k + (seq_row + hd0 + g) * T * D;
@@ -592,19 +770,11 @@ __global__ __launch_bounds__(NTHREADS) void bwd_kernel(
       kf[g][s] = ld_std_bounded<OP>(kh, D, j, T, h, s);
       vf[g][s] = ld_std_bounded<OP>(vh, D, j, T, h, s);
     }
-#pragma unroll
-    for (int db = 0; db < DB; ++db)
-#pragma unroll
-      for (int s = 0; s < AS; ++s) ktf[g][db][s] = ld_colgather<OP>(kh, D, key0, T, db * 32 + n, h, s);
   }
   if (!has_h0) {
     const elem* kh = k + seq_row * T * D;
 #pragma unroll
     for (int s = 0; s < NS; ++s) k0f[s] = ld_std_bounded<OP>(kh, D, j, T, h, s);
-#pragma unroll
-    for (int db = 0; db < DB; ++db)
-#pragma unroll
-      for (int s = 0; s < AS; ++s) k0tf[db][s] = ld_colgather<OP>(kh, D, key0, T, db * 32 + n, h, s);
   }
 
   f32x16 dkt[G][DB], dvt[G][DB], dk0t[DB];
@@ -620,213 +790,177 @@ __global__ __launch_bounds__(NTHREADS) void bwd_kernel(
 
   float ucarry = 0.f;
   const float sl2 = scale * LOG2E;
-  const int qb_lo = (blockIdx.x * NWAVES * TILE) / TILE;
+  // query tiles the workgroup visits, last to first: NB-1 down to the first that reaches its keys
+  const int qb_lo = blockIdx.x * NWAVES;
+  const int ntiles = NB - qb_lo;
 
-  // acc[db] (D x keys) += Y^T X: Y a staged [rows][D]^T LDS tile (rows d, queries in C-layout
-  // order), X a C-layout (queries x keys) tile. With split, X also enters as its rounding residual.
-  auto acc_t = [&](f32x16 (&acc)[DB], const elem* yt, const f32x16& x, bool split) {
+  // Staging of one query tile: Q, Q^T, dO, dO^T of the group (+ head 0's Q, Q^T), lse, dbar.
+  RowTile<elem, D> nQ[NH], ndO[G];
+  ColTile<elem, D> nQt[NH], ndOt[G];
+  float nLse[G], nDb[G];
+  auto load_tile = [&](int qb) {
+    const int qbase = qb * TILE;
 #pragma unroll
-    for (int db = 0; db < DB; ++db)
+    for (int g = 0; g < G; ++g) {
+      const int64_t row = seq_row + hd0 + g;
+      nQ[g].load(q + row * T * D, D, qbase, T, tid);
+      nQt[g].load(qt + row * D * ldt, ldt, qbase, tid);
+      ndO[g].load(dout + row * T * D, D, qbase, T, tid);
+      ndOt[g].load(dot + row * D * ldt, ldt, qbase, tid);
+      const int r = qbase + (tid & (TILE - 1));
+      const int rr = min(r, T - 1);
+      const float lv = lse[row * T + rr], dv_ = dbar[row * T + rr];
+      nLse[g] = r < T ? lv : 0.f;
+      nDb[g] = r < T ? dv_ : 0.f;
+    }
+    if (!has_h0) {
+      nQ[G].load(q + seq_row * T * D, D, qbase, T, tid);
+      nQt[G].load(qt + seq_row * D * ldt, ldt, qbase, tid);
+    }
+  };
+  auto store_tile = [&](int buf) {
 #pragma unroll
-      for (int s = 0; s < AS; ++s) acc[db] = OP::mma(OP::ld_perm(yt, LDV, db * 32 + n, h, s), OP::from_acc(x, s), acc[db]);
-    if constexpr (OP::SPLIT) {
-      if (split) {
-#pragma unroll
-        for (int db = 0; db < DB; ++db)
-#pragma unroll
-          for (int s = 0; s < AS; ++s)
-            acc[db] = OP::mma(OP::ld_perm(yt, LDV, db * 32 + n, h, s), OP::from_acc_lo(x, s), acc[db]);
+    for (int g = 0; g < G; ++g) {
+      nQ[g].template store<LDK>(sQ[buf][g], tid);
+      nQt[g].template store<LDV>(sQt[buf][g], tid);
+      ndO[g].template store<LDK>(sdO[buf][g], tid);
+      ndOt[g].template store<LDV>(sdOt[buf][g], tid);
+      if (tid < TILE) {
+        sLse[buf][g][tid] = nLse[g];
+        sDb[buf][g][tid] = nDb[g];
       }
+    }
+    if (!has_h0) {
+      nQ[G].template store<LDK>(sQ[buf][G], tid);
+      nQt[G].template store<LDV>(sQt[buf][G], tid);
     }
   };
 
-  // dz (C layout, queries x keys) -> LDS -> dQ tile += dz K -> atomics into dq rows of qb. With
-  // split, the rounding residual of dz takes a second pass through LDS.
-  auto dq_update = [&](const f32x16& dzv, const frag (&ktfr)[DB][AS], float* dqh, int qb, bool split) {
-    f32x16 acc[DB];
+  // acc[db] (D x keys) += Y^T X: Y a staged transposed LDS tile (rows d, queries in C-layout
+  // order), X a C-layout (queries x keys) tile; with split, X also enters as its rounding residual.
+  auto acc_t = [&](f32x16 (&acc)[DB], const elem* yt, const f32x16& x, bool split) {
+    frag xf[AS];
 #pragma unroll
-    for (int db = 0; db < DB; ++db) acc[db] = zero16();
-#pragma unroll
-    for (int i = 0; i < 16; ++i) zs[crow(i, h) * LDZ + n] = OP::to_elem(dzv[i]);
-    lds_wave_sync();
+    for (int s = 0; s < AS; ++s) xf[s] = OP::from_acc(x, s);
 #pragma unroll
     for (int db = 0; db < DB; ++db)
 #pragma unroll
-      for (int s = 0; s < AS; ++s) acc[db] = OP::mma(OP::ld_std(zs, LDZ, n, h, s), ktfr[db][s], acc[db]);
+      for (int s = 0; s < AS; ++s) acc[db] = OP::mma(OP::ld_perm(yt, LDV, db * 32 + n, h, s), xf[s], acc[db]);
     if constexpr (OP::SPLIT) {
       if (split) {
-        lds_wave_sync();
 #pragma unroll
-        for (int i = 0; i < 16; ++i) zs[crow(i, h) * LDZ + n] = OP::to_elem_lo(dzv[i]);
-        lds_wave_sync();
+        for (int s = 0; s < AS; ++s) xf[s] = OP::from_acc_lo(x, s);
 #pragma unroll
         for (int db = 0; db < DB; ++db)
 #pragma unroll
-          for (int s = 0; s < AS; ++s) acc[db] = OP::mma(OP::ld_std(zs, LDZ, n, h, s), ktfr[db][s], acc[db]);
+          for (int s = 0; s < AS; ++s) acc[db] = OP::mma(OP::ld_perm(yt, LDV, db * 32 + n, h, s), xf[s], acc[db]);
       }
     }
-#pragma unroll
-    for (int db = 0; db < DB; ++db)
-#pragma unroll
-      for (int i = 0; i < 16; ++i) {
-        const int r = qb * TILE + crow(i, h);
-        if (r < T) atomicAdd(dqh + (int64_t)r * D + db * 32 + n, acc[db][i]);
-      }
-    lds_wave_sync();
   };
 
   // Keys below `exempt` are never selected, so they gather attention from every later query and
   // their dV / dK sums run over all of them: their products take the split operands.
   const bool split_keys = key0 < exempt;
 
-  for (int qb = NB - 1; qb >= qb_lo; --qb) {
+  float hist_next = 0.f;
+  if constexpr (BWD_PIPE) {
+    load_tile(NB - 1);
+    hist_next = carry_col[(int64_t)(NB - 1) * T];
+    store_tile(0);
+    __syncthreads();
+  }
+
+  for (int t = 0; t < ntiles; ++t) {
+    const int qb = NB - 1 - t;
     const int qbase = qb * TILE;
-    __syncthreads();
-#pragma unroll
-    for (int g = 0; g < G; ++g) {
-      const int64_t row = seq_row + hd0 + g;
-      stage_rows<elem, D, LDK>(sQ[g], q + row * T * D, D, qbase, T, tid);
-      stage_cols<elem, D, LDV>(sQt[g], qt + row * D * ldt, ldt, qbase, T, tid);
-      stage_rows<elem, D, LDK>(sdO[g], dout + row * T * D, D, qbase, T, tid);
-      stage_cols<elem, D, LDV>(sdOt[g], dot + row * D * ldt, ldt, qbase, T, tid);
-      if (tid < TILE) {
-        const int r = qbase + tid;
-        sLse[g][tid] = (r < T) ? lse[row * T + r] : 0.f;
-        sDb[g][tid] = (r < T) ? dbar[row * T + r] : 0.f;
+    const int buf = NBUF == 2 ? (t & 1) : 0;
+    float hist;
+    if constexpr (BWD_PIPE) {
+      hist = hist_next;
+      if (t + 1 < ntiles) {
+        load_tile(qb - 1);
+        hist_next = carry_col[(int64_t)(qb - 1) * T];
       }
-    }
-    if (!has_h0) {
-      stage_rows<elem, D, LDK>(sQ[G], q + seq_row * T * D, D, qbase, T, tid);
-      stage_cols<elem, D, LDV>(sQt[G], qt + seq_row * D * ldt, ldt, qbase, T, tid);
-    }
-    __syncthreads();
-    if (qbase + TILE - 1 < key0) continue;   // every query of the tile precedes every key
-    const bool diag = (qbase < key0 + TILE - 1) || (qbase + TILE > T) || (key0 + TILE > T);
-
-    // head 0 logits (queries x keys), selection gate and F (log2 units)
-    const elem* q0s = has_h0 ? sQ[0] : sQ[G];
-    f32x16 l0 = zero16();
-#pragma unroll
-    for (int s = 0; s < NS; ++s) l0 = OP::mma(OP::ld_std(q0s, LDK, n, h, s), has_h0 ? kf[0][s] : k0f[s], l0);
-    f32x16 sel, fs;
-    uint32_t gmask = 0;
-#pragma unroll
-    for (int i = 0; i < 16; ++i) {
-      const int r = qbase + crow(i, h);
-      const float sv = l0[i] * scale;
-      const bool gate = (r < T) && (j >= exempt) && (j < r) && (sv > 0.f);
-      sel[i] = gate ? sv : 0.f;
-      gmask |= gate ? (1u << i) : 0u;
-    }
-    {
-      float gs[4], pg[4];
-#pragma unroll
-      for (int a = 0; a < 4; ++a) gs[a] = ((sel[4 * a] + sel[4 * a + 1]) + sel[4 * a + 2]) + sel[4 * a + 3];
-#pragma unroll
-      for (int a = 0; a < 4; ++a) pg[a] = xor32(gs[a]);
-      float run = (j < T) ? carry[((int64_t)b * NB + qb) * T + j] : 0.f;
-#pragma unroll
-      for (int a = 0; a < 4; ++a) {
-        const float g_lo = h == 0 ? gs[a] : pg[a];   // rows 8a..8a+3
-        const float g_hi = h == 0 ? pg[a] : gs[a];   // rows 8a+4..8a+7
-        float p = (h == 0) ? run : run + g_lo;
-#pragma unroll
-        for (int t = 0; t < 4; ++t) {
-          fs[4 * a + t] = p * LOG2E;
-          p += sel[4 * a + t];
-        }
-        run = (run + g_lo) + g_hi;
-      }
-    }
-
-    f32x16 dzsum = zero16();
-    f32x16 dz0 = zero16();
-#pragma unroll
-    for (int gg = 0; gg < G; ++gg) {
-      const int g = has_h0 ? (gg + 1) % G : gg;   // head 0 last: its dK, dQ wait for g
-      const int64_t row = seq_row + hd0 + g;
-      f32x16 lg;
-      if (has_h0 && g == 0) {
-        lg = l0;
-      } else {
-        lg = zero16();
-#pragma unroll
-        for (int s = 0; s < NS; ++s) lg = OP::mma(OP::ld_std(sQ[g], LDK, n, h, s), kf[g][s], lg);
-      }
-      f32x16 dp = zero16();
-#pragma unroll
-      for (int s = 0; s < NS; ++s) dp = OP::mma(OP::ld_std(sdO[g], LDK, n, h, s), vf[g][s], dp);
-      f32x16 pr, dz;
-#pragma unroll
-      for (int a = 0; a < 4; ++a) {
-        const float4 ls = *reinterpret_cast<const float4*>(&sLse[g][8 * a + 4 * h]);
-        const float4 dbv = *reinterpret_cast<const float4*>(&sDb[g][8 * a + 4 * h]);
-        const float lsv[4] = {ls.x, ls.y, ls.z, ls.w};
-        const float dbs[4] = {dbv.x, dbv.y, dbv.z, dbv.w};
-#pragma unroll
-        for (int t = 0; t < 4; ++t) {
-          const int i = 4 * a + t;
-          float p = fast_exp2(lg[i] * sl2 - fs[i] - lsv[t]);
-          if (diag) {
-            const int r = qbase + crow(i, h);
-            if (j > r || r >= T || j >= T) p = 0.f;
-          }
-          pr[i] = p;
-          dz[i] = p * (dp[i] - dbs[t]);
-        }
-      }
-      // dV^T += dO^T P
-      acc_t(dvt[g], sdOt[g], pr, split_keys);
-#pragma unroll
-      for (int i = 0; i < 16; ++i) dzsum[i] += dz[i];
-      if (has_h0 && g == 0) {
-        dz0 = dz;
-      } else {
-        acc_t(dkt[g], sQt[g], dz, split_keys);
-        dq_update(dz, ktf[g], dq + row * T * D, qb, false);
-      }
-    }
-
-    // U = ucarry + sum over later queries of the tile (reverse exclusive), g = -gate U
-    f32x16 gpath;
-    {
-      float gs[4], pg[4];
-#pragma unroll
-      for (int a = 0; a < 4; ++a) gs[a] = ((dzsum[4 * a + 3] + dzsum[4 * a + 2]) + dzsum[4 * a + 1]) + dzsum[4 * a];
-#pragma unroll
-      for (int a = 0; a < 4; ++a) pg[a] = xor32(gs[a]);
-      float run = ucarry;
-#pragma unroll
-      for (int a = 3; a >= 0; --a) {
-        const float g_lo = h == 0 ? gs[a] : pg[a];
-        const float g_hi = h == 0 ? pg[a] : gs[a];
-        float p = (h == 1) ? run : run + g_hi;
-#pragma unroll
-        for (int t = 3; t >= 0; --t) {
-          const int i = 4 * a + t;
-          gpath[i] = ((gmask >> i) & 1u) ? -p : 0.f;
-          p += dzsum[i];
-        }
-        run = (run + g_hi) + g_lo;
-      }
-      ucarry = run;
-    }
-
-    // g sums dz over every later query of every head: it outgrows the dz tiles, so head 0's
-    // products take it split (the group holding head 0 always, the others when some |g| > 1/4).
-    if (has_h0) {
-      f32x16 dzh;
-#pragma unroll
-      for (int i = 0; i < 16; ++i) dzh[i] = dz0[i] + gpath[i];
-      acc_t(dkt[0], sQt[0], dzh, true);
-      dq_update(dzh, ktf[0], dq + seq_row * T * D, qb, true);
     } else {
-      bool big = false;
+      load_tile(qb);
+      hist = carry_col[(int64_t)qb * T];
+      if (t > 0) __syncthreads();   // every wavefront is done with the previous tile
+      store_tile(0);
+      __syncthreads();
+    }
+    if (qbase + TILE - 1 >= key0) {   // else every query of the tile precedes every key
+      if (h == 0 && j < T) uplane[(int64_t)qb * T + j] = ucarry;
+      const bool diag = (qbase < key0 + TILE - 1) || (qbase + TILE > T) || (key0 + TILE > T);
+
+      const elem* q0s = has_h0 ? sQ[buf][0] : sQ[buf][G];
+      f32x16 l0 = zero16();
 #pragma unroll
-      for (int i = 0; i < 16; ++i) big |= fabsf(gpath[i]) > 0.25f;
-      const bool split_g = __any(big);
-      acc_t(dk0t, sQt[G], gpath, split_g);
-      dq_update(gpath, k0tf, dq + seq_row * T * D, qb, split_g);
+      for (int s = 0; s < NS; ++s) l0 = OP::mma(OP::ld_std(q0s, LDK, n, h, s), has_h0 ? kf[0][s] : k0f[s], l0);
+      f32x16 fs;
+      uint32_t gmask;
+      const bool edge = diag || key0 < exempt;
+      selection_tile(l0, (j < T) ? hist : 0.f, qbase, j, T, exempt, scale, h, edge, fs, gmask);
+
+      f32x16 dzsum = zero16();
+      f32x16 dz0 = zero16();
+#pragma unroll
+      for (int gg = 0; gg < G; ++gg) {
+        const int g = has_h0 ? (gg + 1) % G : gg;   // head 0 last: its dK waits for g
+        f32x16 lg;
+        if (has_h0 && g == 0) {
+          lg = l0;
+        } else {
+          lg = zero16();
+#pragma unroll
+          for (int s = 0; s < NS; ++s) lg = OP::mma(OP::ld_std(sQ[buf][g], LDK, n, h, s), kf[g][s], lg);
+        }
+        f32x16 dp = zero16();
+#pragma unroll
+        for (int s = 0; s < NS; ++s) dp = OP::mma(OP::ld_std(sdO[buf][g], LDK, n, h, s), vf[g][s], dp);
+        f32x16 pr, dz;
+#pragma unroll
+        for (int a = 0; a < 4; ++a) {
+          const float4 ls = *reinterpret_cast<const float4*>(&sLse[buf][g][8 * a + 4 * h]);
+          const float4 dbv = *reinterpret_cast<const float4*>(&sDb[buf][g][8 * a + 4 * h]);
+          const float lsv[4] = {ls.x, ls.y, ls.z, ls.w};
+          const float dbs[4] = {dbv.x, dbv.y, dbv.z, dbv.w};
+#pragma unroll
+          for (int u = 0; u < 4; ++u) {
+            const int i = 4 * a + u;
+            float p = fast_exp2(lg[i] * sl2 - fs[i] - lsv[u]);
+            if (diag) {
+              const int r = qbase + crow(i, h);
+              if (j > r || r >= T || j >= T) p = 0.f;
+            }
+            pr[i] = p;
+            dz[i] = p * (dp[i] - dbs[u]);
+          }
+        }
+        acc_t(dvt[g], sdOt[buf][g], pr, split_keys);   // dV^T += dO^T P
+#pragma unroll
+        for (int i = 0; i < 16; ++i) dzsum[i] += dz[i];
+        if (has_h0 && g == 0) {
+          dz0 = dz;
+        } else {
+          acc_t(dkt[g], sQt[buf][g], dz, split_keys);   // dK^T += Q^T dz
+        }
+      }
+
+      f32x16 gp;
+      ucarry = gpath_tile(dzsum, ucarry, gmask, h, gp);
+      if (has_h0) {
+        f32x16 dzh;
+#pragma unroll
+        for (int i = 0; i < 16; ++i) dzh[i] = dz0[i] + gp[i];
+        acc_t(dkt[0], sQt[buf][0], dzh, true);
+      } else {
+        acc_t(dk0t, sQt[buf][G], gp, big_tile(gp));
+      }
+    }
+    if constexpr (BWD_PIPE) {
+      if constexpr (NBUF == 1) __syncthreads();   // the one buffer is free again
+      if (t + 1 < ntiles) store_tile(NBUF == 2 ? buf ^ 1 : 0);
+      __syncthreads();
     }
   }
 
@@ -857,21 +991,301 @@ __global__ __launch_bounds__(NTHREADS) void bwd_kernel(
   }
 }
 
-// Gradients to the output dtype (bf16 or fp32): dq*scale, dk (+ head 0's share from other groups), dv.
+// ---------------------------------------------------------------------------------------------
+// Backward, query side. grid (ceil(T/128), nseq * H/G); wavefront w owns queries
+// [x*128 + 32w, +32) of heads [gi*G, gi*G+G) (late query blocks launch first) and walks the key
+// tiles up to its diagonal, with Q, dO and the dQ sums in registers. It recomputes P and dz as the
+// key side does, and this group's share of head 0's g from the key side's checkpoint of U plus
+// the suffix inside the tile. dQ = dz K takes dz through a per-wavefront LDS tile (as the A operand)
+// and K^T from LDS (as the B operand).
+
+template <class OP, int D, int G>
+__global__ __launch_bounds__(NTHREADS, SA_BWD_MIN_BLOCKS) void bwd_dq_kernel(
+    const typename OP::elem* __restrict__ q, const typename OP::elem* __restrict__ k,
+    const typename OP::elem* __restrict__ v, const typename OP::elem* __restrict__ kt,
+    const typename OP::elem* __restrict__ dout, const float* __restrict__ lse, const float* __restrict__ dbar,
+    const float* __restrict__ carry, const float* __restrict__ ucheck, float* __restrict__ dq,
+    float* __restrict__ dq0x, int nseq, int H, int T, int64_t ldt, int exempt, float scale) {
+  using elem = typename OP::elem;
+  using frag = typename OP::frag;
+  constexpr int NS = D / OP::KS;
+  constexpr int DB = D / 32;
+  constexpr int LDK = D + OP::KPAD;
+  constexpr int LDKT = TILE + OP::KPAD;
+  constexpr int LDZ = TILE + OP::KPAD;
+  constexpr int AS = OP::acc_steps;
+  constexpr int NH = G + 1;
+  constexpr int TILE_BYTES = (NH * (TILE * LDK + D * LDKT) + G * TILE * LDK) * (int)sizeof(elem);
+  constexpr int NBUF = (BWD_PIPE && 2 * TILE_BYTES <= 120 * 1024) ? 2 : 1;
+
+  __shared__ __attribute__((aligned(16))) elem sK[NBUF][NH][TILE * LDK];
+  __shared__ __attribute__((aligned(16))) elem sKt[NBUF][NH][D * LDKT];
+  __shared__ __attribute__((aligned(16))) elem sV[NBUF][G][TILE * LDK];
+  __shared__ __attribute__((aligned(16))) elem sZ[NWAVES][TILE * LDZ];
+  __shared__ __attribute__((aligned(16))) float sLse[NWAVES][G][TILE];
+  __shared__ __attribute__((aligned(16))) float sDb[NWAVES][G][TILE];
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int n = lane & 31, h = lane >> 5;
+  const int groups = H / G;
+  const int b = blockIdx.y / groups, gi = blockIdx.y % groups;
+  const int hd0 = gi * G;
+  const bool has_h0 = (gi == 0);
+  const int NB = (T + TILE - 1) / TILE;
+  const int qsb = gridDim.x - 1 - blockIdx.x;
+  const int qb = qsb * NWAVES + wave;
+  const int qbase = qb * TILE;
+  const int64_t seq_row = (int64_t)b * H;
+  const int my_end = (qb < NB) ? qb + 1 : 0;
+  const int wg_end = min(qsb * NWAVES + NWAVES - 1, NB - 1) + 1;
+  elem* zs = sZ[wave];
+  // this wavefront's rows of the carry and U checkpoints (key offset added per tile)
+  const int qb_c = qb < NB ? qb : NB - 1;
+  const float* carry_row = carry + ((int64_t)b * NB + qb_c) * T;
+  const float* urow = ucheck + (((int64_t)gi * nseq + b) * NB + qb_c) * T;
+
+  // Query-side operands in registers (A operands: lane = query row).
+  frag qa[G][NS], doa[G][NS], q0a[NS];
+#pragma unroll
+  for (int g = 0; g < G; ++g) {
+    const int64_t row = seq_row + hd0 + g;
+#pragma unroll
+    for (int s = 0; s < NS; ++s) {
+      qa[g][s] = ld_std_bounded<OP>(q + row * T * D, D, qbase + n, T, h, s);
+      doa[g][s] = ld_std_bounded<OP>(dout + row * T * D, D, qbase + n, T, h, s);
+    }
+    if (lane < TILE) {
+      const int r = qbase + lane;
+      sLse[wave][g][lane] = (r < T) ? lse[row * T + r] : 0.f;
+      sDb[wave][g][lane] = (r < T) ? dbar[row * T + r] : 0.f;
+    }
+  }
+  if (!has_h0) {
+#pragma unroll
+    for (int s = 0; s < NS; ++s) q0a[s] = ld_std_bounded<OP>(q + seq_row * T * D, D, qbase + n, T, h, s);
+  }
+
+  f32x16 dqacc[G][DB], dq0acc[DB];
+#pragma unroll
+  for (int g = 0; g < G; ++g)
+#pragma unroll
+    for (int db = 0; db < DB; ++db) dqacc[g][db] = zero16();
+#pragma unroll
+  for (int db = 0; db < DB; ++db) dq0acc[db] = zero16();
+
+  const float sl2 = scale * LOG2E;
+
+  // Staging of one key tile: K, V, K^T of the group (+ head 0's K, K^T).
+  RowTile<elem, D> nK[NH], nV[G];
+  ColTile<elem, D> nKt[NH];
+  auto load_tile = [&](int ktile) {
+    const int kbase = ktile * TILE;
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+      const int64_t row = seq_row + hd0 + g;
+      nK[g].load(k + row * T * D, D, kbase, T, tid);
+      nV[g].load(v + row * T * D, D, kbase, T, tid);
+      nKt[g].load(kt + row * D * ldt, ldt, kbase, tid);
+    }
+    if (!has_h0) {
+      nK[G].load(k + seq_row * T * D, D, kbase, T, tid);
+      nKt[G].load(kt + seq_row * D * ldt, ldt, kbase, tid);
+    }
+  };
+  auto store_tile = [&](int buf) {
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+      nK[g].template store<LDK>(sK[buf][g], tid);
+      nV[g].template store<LDK>(sV[buf][g], tid);
+      nKt[g].template store<LDKT>(sKt[buf][g], tid);
+    }
+    if (!has_h0) {
+      nK[G].template store<LDK>(sK[buf][G], tid);
+      nKt[G].template store<LDKT>(sKt[buf][G], tid);
+    }
+  };
+
+  // acc[db] (queries x D) += X K: X a C-layout (queries x keys) tile, sent through LDS to become
+  // the A operand; K^T (rows d) staged in LDS is the B operand. With split, X's rounding residual
+  // takes a second pass.
+  auto acc_xk = [&](f32x16 (&acc)[DB], const f32x16& x, const elem* ktile, bool split) {
+    frag zf[AS];
+#pragma unroll
+    for (int i = 0; i < 16; ++i) zs[crow(i, h) * LDZ + n] = OP::to_elem(x[i]);
+    lds_wave_sync();
+#pragma unroll
+    for (int s = 0; s < AS; ++s) zf[s] = OP::ld_std(zs, LDZ, n, h, s);
+#pragma unroll
+    for (int db = 0; db < DB; ++db)
+#pragma unroll
+      for (int s = 0; s < AS; ++s) acc[db] = OP::mma(zf[s], OP::ld_std(ktile, LDKT, db * 32 + n, h, s), acc[db]);
+    if constexpr (OP::SPLIT) {
+      if (split) {
+        lds_wave_sync();
+#pragma unroll
+        for (int i = 0; i < 16; ++i) zs[crow(i, h) * LDZ + n] = OP::to_elem_lo(x[i]);
+        lds_wave_sync();
+#pragma unroll
+        for (int s = 0; s < AS; ++s) zf[s] = OP::ld_std(zs, LDZ, n, h, s);
+#pragma unroll
+        for (int db = 0; db < DB; ++db)
+#pragma unroll
+          for (int s = 0; s < AS; ++s) acc[db] = OP::mma(zf[s], OP::ld_std(ktile, LDKT, db * 32 + n, h, s), acc[db]);
+      }
+    }
+    lds_wave_sync();
+  };
+
+  auto key_vals = [&](int ktile, float& hv, float& uv) {
+    const int jj = ktile * TILE + n;
+    hv = (jj < T) ? carry_row[jj] : 0.f;
+    uv = (jj < T) ? urow[jj] : 0.f;
+  };
+
+  float hist_next = 0.f, u_next = 0.f;
+  if constexpr (BWD_PIPE) {
+    load_tile(0);
+    key_vals(0, hist_next, u_next);
+    store_tile(0);
+    __syncthreads();
+  }
+
+  for (int ktile = 0; ktile < wg_end; ++ktile) {
+    const int kbase = ktile * TILE;
+    const int buf = NBUF == 2 ? (ktile & 1) : 0;
+    float hist, uin;
+    if constexpr (BWD_PIPE) {
+      hist = hist_next;
+      uin = u_next;
+      if (ktile + 1 < wg_end) {
+        load_tile(ktile + 1);
+        key_vals(ktile + 1, hist_next, u_next);
+      }
+    } else {
+      load_tile(ktile);
+      key_vals(ktile, hist, uin);
+      if (ktile > 0) __syncthreads();   // every wavefront is done with the previous tile
+      store_tile(0);
+      __syncthreads();
+    }
+    if (ktile < my_end) {
+      const int j = kbase + n;
+      const bool diag = (kbase + TILE - 1 > qbase) || (qbase + TILE > T) || (kbase + TILE > T);
+
+      const elem* k0s = has_h0 ? sK[buf][0] : sK[buf][G];
+      f32x16 l0 = zero16();
+#pragma unroll
+      for (int s = 0; s < NS; ++s) l0 = OP::mma(has_h0 ? qa[0][s] : q0a[s], OP::ld_std(k0s, LDK, n, h, s), l0);
+      f32x16 fs;
+      uint32_t gmask;
+      const bool edge = diag || kbase < exempt;
+      selection_tile(l0, hist, qbase, j, T, exempt, scale, h, edge, fs, gmask);
+
+      f32x16 zsum = zero16();
+      f32x16 dz0 = zero16();
+#pragma unroll
+      for (int gg = 0; gg < G; ++gg) {
+        const int g = has_h0 ? (gg + 1) % G : gg;
+        f32x16 lg;
+        if (has_h0 && g == 0) {
+          lg = l0;
+        } else {
+          lg = zero16();
+#pragma unroll
+          for (int s = 0; s < NS; ++s) lg = OP::mma(qa[g][s], OP::ld_std(sK[buf][g], LDK, n, h, s), lg);
+        }
+        f32x16 dp = zero16();
+#pragma unroll
+        for (int s = 0; s < NS; ++s) dp = OP::mma(doa[g][s], OP::ld_std(sV[buf][g], LDK, n, h, s), dp);
+        f32x16 dz;
+#pragma unroll
+        for (int a = 0; a < 4; ++a) {
+          const float4 ls = *reinterpret_cast<const float4*>(&sLse[wave][g][8 * a + 4 * h]);
+          const float4 dbv = *reinterpret_cast<const float4*>(&sDb[wave][g][8 * a + 4 * h]);
+          const float lsv[4] = {ls.x, ls.y, ls.z, ls.w};
+          const float dbs[4] = {dbv.x, dbv.y, dbv.z, dbv.w};
+#pragma unroll
+          for (int u = 0; u < 4; ++u) {
+            const int i = 4 * a + u;
+            float p = fast_exp2(lg[i] * sl2 - fs[i] - lsv[u]);
+            if (diag) {
+              const int r = qbase + crow(i, h);
+              if (j > r || r >= T || j >= T) p = 0.f;
+            }
+            dz[i] = p * (dp[i] - dbs[u]);
+          }
+        }
+#pragma unroll
+        for (int i = 0; i < 16; ++i) zsum[i] += dz[i];
+        if (has_h0 && g == 0) {
+          dz0 = dz;
+        } else {
+          acc_xk(dqacc[g], dz, sKt[buf][g], false);
+        }
+      }
+
+      f32x16 gp;
+      gpath_tile(zsum, uin, gmask, h, gp);
+      if (has_h0) {
+        f32x16 dzh;
+#pragma unroll
+        for (int i = 0; i < 16; ++i) dzh[i] = dz0[i] + gp[i];
+        acc_xk(dqacc[0], dzh, sKt[buf][0], true);
+      } else {
+        acc_xk(dq0acc, gp, sKt[buf][G], big_tile(gp));
+      }
+    }
+    if constexpr (BWD_PIPE) {
+      if constexpr (NBUF == 1) __syncthreads();   // the one buffer is free again
+      if (ktile + 1 < wg_end) store_tile(NBUF == 2 ? buf ^ 1 : 0);
+      __syncthreads();
+    }
+  }
+
+  if (qb >= NB) return;
+#pragma unroll
+  for (int g = 0; g < G; ++g) {
+    const int64_t row = seq_row + hd0 + g;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      const int r = qbase + crow(i, h);
+      if (r < T) {
+#pragma unroll
+        for (int db = 0; db < DB; ++db) dq[(row * T + r) * D + db * 32 + n] = dqacc[g][db][i];
+      }
+    }
+  }
+  if (!has_h0) {
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      const int r = qbase + crow(i, h);
+      if (r < T) {
+#pragma unroll
+        for (int db = 0; db < DB; ++db) atomicAdd(dq0x + ((int64_t)b * T + r) * D + db * 32 + n, dq0acc[db][i]);
+      }
+    }
+  }
+}
+
+// Gradients to the output dtype (bf16 or fp32): dq*scale, dk, dv, with head 0's dQ and dK shares
+// from the other head groups (dq0x unscaled, dk0x scaled) added to head 0.
 __device__ __forceinline__ void store_grad(uint16_t* p, float x) { *p = OpBF16::to_elem(x); }
 __device__ __forceinline__ void store_grad(float* p, float x) { *p = x; }
 
 template <typename OUT>
 __global__ __launch_bounds__(NTHREADS) void bwd_finish_kernel(
     const float* __restrict__ dq32, const float* __restrict__ dk32, const float* __restrict__ dv32,
-    const float* __restrict__ dk0x, OUT* __restrict__ dq, OUT* __restrict__ dk, OUT* __restrict__ dv, int H,
-    int64_t TD, int64_t total, float scale) {
+    const float* __restrict__ dq0x, const float* __restrict__ dk0x, OUT* __restrict__ dq, OUT* __restrict__ dk,
+    OUT* __restrict__ dv, int H, int64_t TD, int64_t total, float scale) {
   for (int64_t e = (int64_t)blockIdx.x * NTHREADS + threadIdx.x; e < total; e += (int64_t)gridDim.x * NTHREADS) {
     const int64_t row = e / TD;          // b*H + head
     const int64_t off = e - row * TD;
-    float kv = dk32[e];
-    if (row % H == 0) kv += dk0x[(row / H) * TD + off];
-    store_grad(dq + e, dq32[e] * scale);
+    float qv = dq32[e], kv = dk32[e];
+    if (row % H == 0) {
+      qv += dq0x[(row / H) * TD + off];
+      kv += dk0x[(row / H) * TD + off];
+    }
+    store_grad(dq + e, qv * scale);
     store_grad(dk + e, kv);
     store_grad(dv + e, dv32[e]);
   }
@@ -999,36 +1413,62 @@ int forward_impl(const void* q_, const void* k_, const void* v_, float* out, flo
   return launch_status();
 }
 
+// Heads per wavefront of the backward kernels: a group shares head 0's selection work (its logits,
+// the history F and the g products), so wider groups amortise it, within the register budget.
+#ifndef SA_BWD_GROUP_DEFAULT
+#define SA_BWD_GROUP_DEFAULT 1
+#endif
+int bwd_group(int dtype, int64_t D, int64_t heads, int requested) {
+  int g = requested > 0 ? requested : SA_BWD_GROUP_DEFAULT;
+  const int cap = (dtype == SA_DTYPE_BF16 && D <= 32) ? 2 : 1;
+  g = g > cap ? cap : g;
+  while (g > 1 && (heads % g != 0)) g >>= 1;
+  return g < 1 ? 1 : g;
+}
+
 struct BwdLayout {
-  int64_t qt, dot, lse, dbar, dq, dk, dv, dk0x, total;
+  int64_t qt, dot, kt, lse, dbar, dq, dk, dv, dq0x, dk0x, ucheck, total;
 };
 
-BwdLayout bwd_layout(int64_t nseq, int64_t heads, int64_t t, int64_t D, int64_t esize) {
-  const int64_t R = nseq * heads, ldt = sa_transposed_ld(t);
+// Workspace of sa_backward: transposed Q, dO, K; row statistics; fp32 gradient sums; head 0's
+// shares from other groups; the selection-suffix checkpoints (one plane per head group).
+BwdLayout bwd_layout(int64_t nseq, int64_t heads, int64_t t, int64_t D, int64_t esize, int64_t G) {
+  const int64_t R = nseq * heads, ldt = sa_transposed_ld(t), NB = (t + TILE - 1) / TILE;
   BwdLayout L;
   int64_t off = 0;
   auto take = [&](int64_t bytes) { int64_t o = off; off = align_up(off + bytes, 256); return o; };
   L.qt = take(R * D * ldt * esize);
   L.dot = take(R * D * ldt * esize);
+  L.kt = take(R * D * ldt * esize);
   L.lse = take(R * t * 4);
   L.dbar = take(R * t * 4);
   L.dq = take(R * t * D * 4);
   L.dk = take(R * t * D * 4);
   L.dv = take(R * t * D * 4);
+  L.dq0x = take(nseq * t * D * 4);
   L.dk0x = take(nseq * t * D * 4);
+  L.ucheck = take((heads / G) * nseq * NB * t * 4);
   L.total = off;
   return L;
 }
 
 template <class OP, int D, int G>
 void launch_bwd(const typename OP::elem* q, const typename OP::elem* k, const typename OP::elem* v,
-                const typename OP::elem* qt, const typename OP::elem* dout, const typename OP::elem* dot,
-                const float* lse, const float* dbar, const float* carry, float* dq, float* dk, float* dv,
-                float* dk0x, int nseq, int H, int T, int64_t ldt, int exempt, float scale, hipStream_t st) {
+                const typename OP::elem* qt, const typename OP::elem* kt, const typename OP::elem* dout,
+                const typename OP::elem* dot, const float* lse, const float* dbar, const float* carry, float* ucheck,
+                float* dq, float* dk, float* dv, float* dq0x, float* dk0x, int nseq, int H, int T, int64_t ldt,
+                int exempt, float scale, hipStream_t st) {
   dim3 grid((unsigned)cdiv(T, NWAVES * TILE), (unsigned)(nseq * (H / G)));
-  TimedLaunch timed(SA_KERNEL_BACKWARD, st);
-  hipLaunchKernelGGL((bwd_kernel<OP, D, G>), grid, dim3(NTHREADS), 0, st, q, k, v, qt, dout, dot, lse, dbar, carry,
-                     dq, dk, dv, dk0x, H, T, ldt, exempt, scale);
+  {
+    TimedLaunch timed(SA_KERNEL_BACKWARD, st);
+    hipLaunchKernelGGL((bwd_kv_kernel<OP, D, G>), grid, dim3(NTHREADS), 0, st, q, k, v, qt, dout, dot, lse, dbar,
+                       carry, ucheck, dk, dv, dk0x, nseq, H, T, ldt, exempt, scale);
+  }
+  {
+    TimedLaunch timed(SA_KERNEL_BACKWARD_DQ, st);
+    hipLaunchKernelGGL((bwd_dq_kernel<OP, D, G>), grid, dim3(NTHREADS), 0, st, q, k, v, kt, dout, lse, dbar, carry,
+                       ucheck, dq, dq0x, nseq, H, T, ldt, exempt, scale);
+  }
 }
 
 template <class OP, int D>
@@ -1041,46 +1481,52 @@ int backward_impl(const void* q_, const void* k_, const void* v_, const float* o
   const elem* k = static_cast<const elem*>(k_);
   const elem* v = static_cast<const elem*>(v_);
   const elem* dout = static_cast<const elem*>(dout_);
+  const int dtype = sizeof(elem) == 2 ? SA_DTYPE_BF16 : SA_DTYPE_F32;
+  const int G = bwd_group(dtype, D, H, group);
   const int64_t R = (int64_t)nseq * H, ldt = sa_transposed_ld(T);
-  const BwdLayout L = bwd_layout(nseq, H, T, D, sizeof(elem));
+  const BwdLayout L = bwd_layout(nseq, H, T, D, sizeof(elem), G);
   char* base = static_cast<char*>(ws);
   elem* qt = reinterpret_cast<elem*>(base + L.qt);
   elem* dot = reinterpret_cast<elem*>(base + L.dot);
+  elem* kt = reinterpret_cast<elem*>(base + L.kt);
   float* lse = reinterpret_cast<float*>(base + L.lse);
   float* dbar = reinterpret_cast<float*>(base + L.dbar);
   float* dq32 = reinterpret_cast<float*>(base + L.dq);
   float* dk32 = reinterpret_cast<float*>(base + L.dk);
   float* dv32 = reinterpret_cast<float*>(base + L.dv);
+  float* dq0x = reinterpret_cast<float*>(base + L.dq0x);
   float* dk0x = reinterpret_cast<float*>(base + L.dk0x);
+  float* ucheck = reinterpret_cast<float*>(base + L.ucheck);
 
   dim3 gt((unsigned)cdiv(ldt, 64), (unsigned)R);
   hipLaunchKernelGGL((transpose_kernel<elem, D>), gt, dim3(NTHREADS), 0, st, q, qt, T, ldt);
   hipLaunchKernelGGL((transpose_kernel<elem, D>), gt, dim3(NTHREADS), 0, st, dout, dot, T, ldt);
+  hipLaunchKernelGGL((transpose_kernel<elem, D>), gt, dim3(NTHREADS), 0, st, k, kt, T, ldt);
   hipLaunchKernelGGL((bwd_rowstats_kernel<OP, D>), dim3((unsigned)cdiv(R * T, NTHREADS)), dim3(NTHREADS), 0, st,
                      dout, out, rmax, rden, lse, dbar, R * T);
-  // dq32 and dk0x are atomic targets
-  hipLaunchKernelGGL(fill_zero_kernel, dim3(1024), dim3(NTHREADS), 0, st, reinterpret_cast<float4*>(dq32),
-                     (int64_t)(R * T * D / 4));
+  // head 0's shares from the other groups are atomic targets (one add per element and group)
+  hipLaunchKernelGGL(fill_zero_kernel, dim3(256), dim3(NTHREADS), 0, st, reinterpret_cast<float4*>(dq0x),
+                     (int64_t)((int64_t)nseq * T * D / 4));
   hipLaunchKernelGGL(fill_zero_kernel, dim3(256), dim3(NTHREADS), 0, st, reinterpret_cast<float4*>(dk0x),
                      (int64_t)((int64_t)nseq * T * D / 4));
-  const int dtype = sizeof(elem) == 2 ? SA_DTYPE_BF16 : SA_DTYPE_F32;
-  const int G = auto_group(dtype, D, H, group, true);
-  if (G == 2) {
-    if constexpr (sizeof(elem) == 2 && D <= 32)
-      launch_bwd<OP, D, 2>(q, k, v, qt, dout, dot, lse, dbar, carry, dq32, dk32, dv32, dk0x, nseq, H, T, ldt, exempt,
-                           scale, st);
+#define SA_LAUNCH_BWD(GG)                                                                                          \
+  launch_bwd<OP, D, GG>(q, k, v, qt, kt, dout, dot, lse, dbar, carry, ucheck, dq32, dk32, dv32, dq0x, dk0x, nseq, H, \
+                        T, ldt, exempt, scale, st)
+  if constexpr (sizeof(elem) == 2 && D <= 32) {
+    if (G == 2) SA_LAUNCH_BWD(2);
+    else SA_LAUNCH_BWD(1);
   } else {
-    launch_bwd<OP, D, 1>(q, k, v, qt, dout, dot, lse, dbar, carry, dq32, dk32, dv32, dk0x, nseq, H, T, ldt, exempt,
-                         scale, st);
+    SA_LAUNCH_BWD(1);
   }
+#undef SA_LAUNCH_BWD
   const int64_t total = R * T * D;
   const dim3 fgrid((unsigned)std::min<int64_t>(cdiv(total, NTHREADS), 8192));
   if (grad_dtype == SA_DTYPE_F32)
-    hipLaunchKernelGGL((bwd_finish_kernel<float>), fgrid, dim3(NTHREADS), 0, st, dq32, dk32, dv32, dk0x,
+    hipLaunchKernelGGL((bwd_finish_kernel<float>), fgrid, dim3(NTHREADS), 0, st, dq32, dk32, dv32, dq0x, dk0x,
                        static_cast<float*>(dq_), static_cast<float*>(dk_), static_cast<float*>(dv_), H,
                        (int64_t)T * D, total, scale);
   else
-    hipLaunchKernelGGL((bwd_finish_kernel<uint16_t>), fgrid, dim3(NTHREADS), 0, st, dq32, dk32, dv32, dk0x,
+    hipLaunchKernelGGL((bwd_finish_kernel<uint16_t>), fgrid, dim3(NTHREADS), 0, st, dq32, dk32, dv32, dq0x, dk0x,
                        static_cast<uint16_t*>(dq_), static_cast<uint16_t*>(dk_), static_cast<uint16_t*>(dv_), H,
                        (int64_t)T * D, total, scale);
   return launch_status();
@@ -1181,8 +1627,10 @@ int sa_forward(const void* q, const void* k, const void* v, float* out, float* r
 #undef SA_FWD
 }
 
-int64_t sa_backward_workspace_bytes(int64_t nseq, int64_t heads, int64_t t, int64_t head_dim, int dtype) {
-  return bwd_layout(nseq, heads, t, head_dim, dtype == SA_DTYPE_BF16 ? 2 : 4).total;
+int64_t sa_backward_workspace_bytes(int64_t nseq, int64_t heads, int64_t t, int64_t head_dim, int dtype, int group) {
+  if (!valid_dims(nseq, heads, t) || (dtype != SA_DTYPE_BF16 && dtype != SA_DTYPE_F32)) return -1;
+  return bwd_layout(nseq, heads, t, head_dim, dtype == SA_DTYPE_BF16 ? 2 : 4, bwd_group(dtype, head_dim, heads, group))
+      .total;
 }
 
 int sa_backward(const void* q, const void* k, const void* v, const float* out, const void* dout, const float* rmax,
@@ -1196,7 +1644,8 @@ int sa_backward(const void* q, const void* k, const void* v, const float* out, c
   if (dtype != SA_DTYPE_BF16 && dtype != SA_DTYPE_F32) return SA_ERR_DTYPE;
   if (grad_dtype != SA_DTYPE_BF16 && grad_dtype != SA_DTYPE_F32) return SA_ERR_DTYPE;
   if (head_dim != 32 && head_dim != 64 && head_dim != 128) return SA_ERR_HEAD_DIM;
-  if (workspace_bytes < sa_backward_workspace_bytes(nseq, heads, t, head_dim, dtype)) return SA_ERR_WORKSPACE;
+  if (group < 0 || workspace_bytes < sa_backward_workspace_bytes(nseq, heads, t, head_dim, dtype, group))
+    return SA_ERR_WORKSPACE;
   hipStream_t st = static_cast<hipStream_t>(stream);
   const int ns = (int)nseq, H = (int)heads, T = (int)t;
 #define SA_BWD(OPT, DD) \

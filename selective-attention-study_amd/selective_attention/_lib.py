@@ -12,7 +12,9 @@ import os
 import threading
 
 LIB_NAME = "libsa_hip.so"
-LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), LIB_NAME)
+# SA_HIP_LIBRARY names another build of the same library (for example one compiled with other
+# tile or group defaults); by default the in-tree build next to this file is loaded.
+LIB_PATH = os.environ.get("SA_HIP_LIBRARY") or os.path.join(os.path.dirname(os.path.abspath(__file__)), LIB_NAME)
 
 DTYPE_BF16 = 0
 DTYPE_F32 = 1
@@ -21,6 +23,7 @@ DTYPE_F32 = 1
 KERNEL_FORWARD = 0
 KERNEL_BACKWARD = 1
 KERNEL_SELECTION = 2
+KERNEL_BACKWARD_DQ = 3
 
 # Every function the header declares, with its ctypes signature.
 _P = ctypes.c_void_p
@@ -36,7 +39,7 @@ SIGNATURES = {
     "sa_forward_workspace_bytes": (_I64, [_I64, _I64, _I64, _I64, _I]),
     "sa_forward": (_I, [_P, _P, _P, _P, _P, _P, _P, _P, _P, _I64, _P, _I64,
                         _I64, _I64, _I64, _I64, _I64, _I64, _F, _I, _I, _I, _I, _I64, _P]),
-    "sa_backward_workspace_bytes": (_I64, [_I64, _I64, _I64, _I64, _I]),
+    "sa_backward_workspace_bytes": (_I64, [_I64, _I64, _I64, _I64, _I, _I]),
     "sa_backward": (_I, [_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _I64,
                          _I64, _I64, _I64, _I64, _F, _I, _I, _I, _I, _P]),
 }

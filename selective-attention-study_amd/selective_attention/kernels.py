@@ -323,7 +323,7 @@ class _SelectiveAttentionFn(torch.autograd.Function):
         dq = torch.empty(qs.shape, device=dev, dtype=gdt)
         dk = torch.empty(ks.shape, device=dev, dtype=gdt)
         dv = torch.empty(vs.shape, device=dev, dtype=gdt)
-        ws_bytes = lib.sa_backward_workspace_bytes(batch, heads, seq, kdim, dtype)
+        ws_bytes = lib.sa_backward_workspace_bytes(batch, heads, seq, kdim, dtype, group)
         ws = torch.empty(int(ws_bytes), device=dev, dtype=torch.uint8)
         with torch.cuda.device(dev):
             _lib.check(lib.sa_backward(

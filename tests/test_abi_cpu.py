@@ -45,7 +45,7 @@ def test_workspace_sizes():
     assert lib.sa_transposed_ld(1) == 64 and lib.sa_transposed_ld(64) == 64 and lib.sa_transposed_ld(65) == 128
     fw = lib.sa_forward_workspace_bytes(1, 16, 16384, 64, 0)
     assert fw >= 16 * 64 * 16384 * 2 and fw % 256 == 0
-    bw = lib.sa_backward_workspace_bytes(1, 16, 16384, 64, 0)
+    bw = lib.sa_backward_workspace_bytes(1, 16, 16384, 64, 0, 0)
     assert bw >= 16 * 16384 * 64 * 4 * 3    # dq, dk, dv fp32 at least
 
 
