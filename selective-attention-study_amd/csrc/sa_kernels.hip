@@ -34,6 +34,7 @@
 #include <math.h>
 #include <algorithm>
 #include <mutex>
+#include <type_traits>
 #include <utility>
 #include <vector>
 
@@ -61,7 +62,22 @@ __device__ __forceinline__ f32x16 zero16() {
 
 __device__ __forceinline__ float xor32(float x) { return __shfl_xor(x, 32); }
 
+// The values of lanes 0-31 (lo) and of lanes 32-63 (hi) of the same column, in every lane
+// (one v_permlane32_swap).
+struct Halves {
+  float lo, hi;
+};
+__device__ __forceinline__ Halves halves(float x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_int(x), __float_as_int(x), false, false);
+  return {__int_as_float(r[0]), __int_as_float(r[1])};
+}
+
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+
+// The wavefront index within the workgroup, as a value the compiler knows is uniform across the
+// wavefront (threadIdx.x / 64 is, but divergence analysis cannot see it): tile flags derived from
+// it become scalar branches instead of per-lane exec masks.
+__device__ __forceinline__ int wave_id() { return __builtin_amdgcn_readfirstlane(threadIdx.x >> 6); }
 
 // Wavefront-local ordering of LDS traffic (writes by some lanes, reads by others).
 __device__ __forceinline__ void lds_wave_sync() {
@@ -338,7 +354,7 @@ __global__ __launch_bounds__(NTHREADS) void sel_colsum_kernel(
   using elem = typename OP::elem;
   using frag = typename OP::frag;
   constexpr int NS = D / OP::KS;
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63, wave = wave_id();
   const int n = lane & 31, h = lane >> 5;
   const int NKT = (Tk + TILE - 1) / TILE;
   const int NBq = (Tq + TILE - 1) / TILE;
@@ -415,7 +431,7 @@ __global__ __launch_bounds__(NTHREADS) void fwd_kernel(
   __shared__ __attribute__((aligned(16))) elem sK[G + 1][TILE * LDK];
   __shared__ __attribute__((aligned(16))) elem sVt[G][D * LDV];
 
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63, wave = wave_id();
   const int n = lane & 31, h = lane >> 5;
   const int groups = H / G;
   const int b = blockIdx.y / groups, gi = blockIdx.y % groups;
@@ -626,81 +642,93 @@ __global__ __launch_bounds__(NTHREADS) void fill_zero_kernel(float4* __restrict_
 #define SA_BWD_MIN_BLOCKS 1
 #endif
 constexpr bool BWD_PIPE = SA_BWD_PIPE != 0;
+// A second, mask-free copy of the tile body for interior tiles; kept to bf16 head dims <= 64,
+// where the registers allow it (the head-dim-128 backward with both copies is also beyond what
+// this compiler's AGPR rewrite pass handles).
+template <class OP, int D>
+constexpr bool split_body() { return sizeof(typename OP::elem) == 2 && D <= 64; }
 
 // ---------------------------------------------------------------------------------------------
 // Backward helpers on (queries x keys) C-layout tiles: lane n holds key j = key0 + n, rows are the
 // queries qbase + crow(i, h), i = 0..15 (h = lane / 32).
 
-// Head 0's selection on a tile of its raw logits l0: S = relu(s l0) where exempt <= j < r < T,
-// the gate bits, and the history F[r, j] = hist_in + sum of S over the tile's earlier rows, in
-// log2 units (the running sum runs down the rows; the two half-wavefronts swap partial sums).
-// `edge` (wave-uniform) marks tiles where some pair fails exempt <= j < r < T; elsewhere the gate
-// is the sign of the logit alone.
-__device__ __forceinline__ void selection_tile(const f32x16& l0, float hist_in, int qbase, int j, int T,
-                                               int exempt, float scale, int h, bool edge, f32x16& fs,
-                                               uint32_t& gmask) {
-  f32x16 sel;
-  gmask = 0;
-  if (edge) {
+// Head 0's selection on a tile of its raw logits l0, in log2 units: sel = relu(s log2e l0) where
+// exempt <= j < r < T, and the history F[r, j] = hist2 + sum of sel over the tile's earlier rows
+// (the running sum runs down the rows; the half-wavefronts exchange partial sums). The gate of
+// the gradient path is sel > 0. EDGE (wave-uniform) marks tiles where some pair fails
+// exempt <= j < r < T; elsewhere the gate is the sign of the logit alone.
+template <bool EDGE>
+__device__ __forceinline__ void selection_tile(const f32x16& l0, float hist2, int qbase, int j, int T, int exempt,
+                                               float sl2, int h, f32x16& fs, f32x16& sel) {
 #pragma unroll
-    for (int i = 0; i < 16; ++i) {
+  for (int i = 0; i < 16; ++i) {
+    const float sv = l0[i] * sl2;
+    if constexpr (EDGE) {
       const int r = qbase + crow(i, h);
-      const float sv = l0[i] * scale;
-      const bool gate = (r < T) && (j >= exempt) && (j < r) && (sv > 0.f);
-      sel[i] = gate ? sv : 0.f;
-      gmask |= gate ? (1u << i) : 0u;
-    }
-  } else {
-#pragma unroll
-    for (int i = 0; i < 16; ++i) {
-      const float sv = l0[i] * scale;
+      const bool pair = (r < T) && (j >= exempt) && (j < r);
+      sel[i] = (pair && sv > 0.f) ? sv : 0.f;
+    } else {
       sel[i] = fmaxf(sv, 0.f);
-      gmask |= sv > 0.f ? (1u << i) : 0u;
     }
   }
-  float gs[4], pg[4];
-#pragma unroll
-  for (int a = 0; a < 4; ++a) gs[a] = ((sel[4 * a] + sel[4 * a + 1]) + sel[4 * a + 2]) + sel[4 * a + 3];
-#pragma unroll
-  for (int a = 0; a < 4; ++a) pg[a] = xor32(gs[a]);
-  float run = hist_in;
+  float run = hist2;
 #pragma unroll
   for (int a = 0; a < 4; ++a) {
-    const float g_lo = h == 0 ? gs[a] : pg[a];   // rows 8a..8a+3
-    const float g_hi = h == 0 ? pg[a] : gs[a];   // rows 8a+4..8a+7
-    float p = (h == 0) ? run : run + g_lo;
+    const Halves g = halves(((sel[4 * a] + sel[4 * a + 1]) + sel[4 * a + 2]) + sel[4 * a + 3]);
+    float p = (h == 0) ? run : run + g.lo;   // rows 8a..8a+3 sit in the low half, 8a+4.. in the high
 #pragma unroll
     for (int t = 0; t < 4; ++t) {
-      fs[4 * a + t] = p * LOG2E;
+      fs[4 * a + t] = p;
       p += sel[4 * a + t];
     }
-    run = (run + g_lo) + g_hi;
+    run = (run + g.lo) + g.hi;
   }
 }
 
 // Selection gradient path: U[r, j] = u_in + sum of z over the tile's later rows, and
-// g = -gate * U. Returns u_in + the sum over the whole tile (U entering the tile above).
-__device__ __forceinline__ float gpath_tile(const f32x16& z, float u_in, uint32_t gmask, int h, f32x16& gp) {
-  float gs[4], pg[4];
-#pragma unroll
-  for (int a = 0; a < 4; ++a) gs[a] = ((z[4 * a + 3] + z[4 * a + 2]) + z[4 * a + 1]) + z[4 * a];
-#pragma unroll
-  for (int a = 0; a < 4; ++a) pg[a] = xor32(gs[a]);
+// g = -[sel > 0] U. Returns u_in + the sum over the whole tile (U entering the tile above).
+__device__ __forceinline__ float gpath_tile(const f32x16& z, float u_in, const f32x16& sel, int h, f32x16& gp) {
   float run = u_in;
 #pragma unroll
   for (int a = 3; a >= 0; --a) {
-    const float g_lo = h == 0 ? gs[a] : pg[a];
-    const float g_hi = h == 0 ? pg[a] : gs[a];
-    float p = (h == 1) ? run : run + g_hi;
+    const Halves g = halves(((z[4 * a + 3] + z[4 * a + 2]) + z[4 * a + 1]) + z[4 * a]);
+    float p = (h == 1) ? run : run + g.hi;
 #pragma unroll
     for (int t = 3; t >= 0; --t) {
       const int i = 4 * a + t;
-      gp[i] = ((gmask >> i) & 1u) ? -p : 0.f;
+      gp[i] = sel[i] > 0.f ? -p : 0.f;
       p += z[i];
     }
-    run = (run + g_hi) + g_lo;
+    run = (run + g.hi) + g.lo;
   }
   return run;
+}
+
+// P = exp2(s log2e lg - F - lse) and dz = P (dp - dbar) on a tile; lse and dbar of the tile's rows
+// come from LDS (4 consecutive rows per float4). MASK (wave-uniform) zeroes pairs outside
+// j <= r < T, j < T.
+template <bool MASK>
+__device__ __forceinline__ void p_dz_tile(const f32x16& lg, const f32x16& dp, const f32x16& fs, const float* slse,
+                                          const float* sdb, float sl2, int qbase, int j, int T, int h, f32x16& pr,
+                                          f32x16& dz) {
+#pragma unroll
+  for (int a = 0; a < 4; ++a) {
+    const float4 ls = *reinterpret_cast<const float4*>(slse + 8 * a + 4 * h);
+    const float4 dbv = *reinterpret_cast<const float4*>(sdb + 8 * a + 4 * h);
+    const float lsv[4] = {ls.x, ls.y, ls.z, ls.w};
+    const float dbs[4] = {dbv.x, dbv.y, dbv.z, dbv.w};
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+      const int i = 4 * a + t;
+      float p = fast_exp2(fmaf(lg[i], sl2, -(fs[i] + lsv[t])));
+      if constexpr (MASK) {
+        const int r = qbase + crow(i, h);
+        p = (j <= r && r < T && j < T) ? p : 0.f;
+      }
+      pr[i] = p;
+      dz[i] = p * (dp[i] - dbs[t]);
+    }
+  }
 }
 
 // Whether some |g| of the wavefront's tile is large enough for the split-operand products: g sums
@@ -735,6 +763,7 @@ __global__ __launch_bounds__(NTHREADS, SA_BWD_MIN_BLOCKS) void bwd_kv_kernel(
   constexpr int LDV = TILE + OP::TPAD;
   constexpr int AS = OP::acc_steps;
   constexpr int NH = G + 1;   // staged heads: the group, then head 0 when outside the group
+  constexpr bool SPLIT_BODY = split_body<OP, D>();
   // two buffers (the tile being computed, the next one being written) when they fit in LDS
   constexpr int TILE_BYTES = (NH * (TILE * LDK + D * LDV) + G * (TILE * LDK + D * LDV)) * (int)sizeof(elem);
   constexpr int NBUF = (BWD_PIPE && 2 * TILE_BYTES <= 120 * 1024) ? 2 : 1;
@@ -746,7 +775,7 @@ __global__ __launch_bounds__(NTHREADS, SA_BWD_MIN_BLOCKS) void bwd_kv_kernel(
   __shared__ __attribute__((aligned(16))) float sLse[NBUF][G][TILE];
   __shared__ __attribute__((aligned(16))) float sDb[NBUF][G][TILE];
 
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63, wave = wave_id();
   const int n = lane & 31, h = lane >> 5;
   const int groups = H / G;
   const int b = blockIdx.y / groups, gi = blockIdx.y % groups;
@@ -890,72 +919,61 @@ __global__ __launch_bounds__(NTHREADS, SA_BWD_MIN_BLOCKS) void bwd_kv_kernel(
     }
     if (qbase + TILE - 1 >= key0) {   // else every query of the tile precedes every key
       if (h == 0 && j < T) uplane[(int64_t)qb * T + j] = ucarry;
-      const bool diag = (qbase < key0 + TILE - 1) || (qbase + TILE > T) || (key0 + TILE > T);
+      // tile body; EDGE: some pair of the tile is masked (diagonal, sequence end) or exempt
+      auto body = [&](auto edge_tag) {
+        constexpr bool EDGE = decltype(edge_tag)::value;
+        const elem* q0s = has_h0 ? sQ[buf][0] : sQ[buf][G];
+        f32x16 l0 = zero16();
+#pragma unroll
+        for (int s = 0; s < NS; ++s) l0 = OP::mma(OP::ld_std(q0s, LDK, n, h, s), has_h0 ? kf[0][s] : k0f[s], l0);
+        f32x16 fs, sel;
+        selection_tile<EDGE>(l0, (j < T) ? hist * LOG2E : 0.f, qbase, j, T, exempt, sl2, h, fs, sel);
 
-      const elem* q0s = has_h0 ? sQ[buf][0] : sQ[buf][G];
-      f32x16 l0 = zero16();
+        f32x16 dzsum, dz0;
 #pragma unroll
-      for (int s = 0; s < NS; ++s) l0 = OP::mma(OP::ld_std(q0s, LDK, n, h, s), has_h0 ? kf[0][s] : k0f[s], l0);
-      f32x16 fs;
-      uint32_t gmask;
-      const bool edge = diag || key0 < exempt;
-      selection_tile(l0, (j < T) ? hist : 0.f, qbase, j, T, exempt, scale, h, edge, fs, gmask);
-
-      f32x16 dzsum = zero16();
-      f32x16 dz0 = zero16();
+        for (int gg = 0; gg < G; ++gg) {
+          const int g = has_h0 ? (gg + 1) % G : gg;   // head 0 last: its dK waits for g
+          f32x16 lg;
+          if (has_h0 && g == 0) {
+            lg = l0;
+          } else {
+            lg = zero16();
 #pragma unroll
-      for (int gg = 0; gg < G; ++gg) {
-        const int g = has_h0 ? (gg + 1) % G : gg;   // head 0 last: its dK waits for g
-        f32x16 lg;
-        if (has_h0 && g == 0) {
-          lg = l0;
-        } else {
-          lg = zero16();
+            for (int s = 0; s < NS; ++s) lg = OP::mma(OP::ld_std(sQ[buf][g], LDK, n, h, s), kf[g][s], lg);
+          }
+          f32x16 dp = zero16();
 #pragma unroll
-          for (int s = 0; s < NS; ++s) lg = OP::mma(OP::ld_std(sQ[buf][g], LDK, n, h, s), kf[g][s], lg);
-        }
-        f32x16 dp = zero16();
+          for (int s = 0; s < NS; ++s) dp = OP::mma(OP::ld_std(sdO[buf][g], LDK, n, h, s), vf[g][s], dp);
+          f32x16 pr, dz;
+          p_dz_tile<EDGE>(lg, dp, fs, sLse[buf][g], sDb[buf][g], sl2, qbase, j, T, h, pr, dz);
+          acc_t(dvt[g], sdOt[buf][g], pr, split_keys);   // dV^T += dO^T P
+          if (gg == 0) {
+            dzsum = dz;
+          } else {
 #pragma unroll
-        for (int s = 0; s < NS; ++s) dp = OP::mma(OP::ld_std(sdO[buf][g], LDK, n, h, s), vf[g][s], dp);
-        f32x16 pr, dz;
-#pragma unroll
-        for (int a = 0; a < 4; ++a) {
-          const float4 ls = *reinterpret_cast<const float4*>(&sLse[buf][g][8 * a + 4 * h]);
-          const float4 dbv = *reinterpret_cast<const float4*>(&sDb[buf][g][8 * a + 4 * h]);
-          const float lsv[4] = {ls.x, ls.y, ls.z, ls.w};
-          const float dbs[4] = {dbv.x, dbv.y, dbv.z, dbv.w};
-#pragma unroll
-          for (int u = 0; u < 4; ++u) {
-            const int i = 4 * a + u;
-            float p = fast_exp2(lg[i] * sl2 - fs[i] - lsv[u]);
-            if (diag) {
-              const int r = qbase + crow(i, h);
-              if (j > r || r >= T || j >= T) p = 0.f;
-            }
-            pr[i] = p;
-            dz[i] = p * (dp[i] - dbs[u]);
+            for (int i = 0; i < 16; ++i) dzsum[i] += dz[i];
+          }
+          if (has_h0 && g == 0) {
+            dz0 = dz;
+          } else {
+            acc_t(dkt[g], sQt[buf][g], dz, split_keys);   // dK^T += Q^T dz
           }
         }
-        acc_t(dvt[g], sdOt[buf][g], pr, split_keys);   // dV^T += dO^T P
-#pragma unroll
-        for (int i = 0; i < 16; ++i) dzsum[i] += dz[i];
-        if (has_h0 && g == 0) {
-          dz0 = dz;
-        } else {
-          acc_t(dkt[g], sQt[buf][g], dz, split_keys);   // dK^T += Q^T dz
-        }
-      }
 
-      f32x16 gp;
-      ucarry = gpath_tile(dzsum, ucarry, gmask, h, gp);
-      if (has_h0) {
-        f32x16 dzh;
+        f32x16 gp;
+        ucarry = gpath_tile(dzsum, ucarry, sel, h, gp);
+        if (has_h0) {
+          f32x16 dzh;
 #pragma unroll
-        for (int i = 0; i < 16; ++i) dzh[i] = dz0[i] + gp[i];
-        acc_t(dkt[0], sQt[buf][0], dzh, true);
-      } else {
-        acc_t(dk0t, sQt[buf][G], gp, big_tile(gp));
-      }
+          for (int i = 0; i < 16; ++i) dzh[i] = dz0[i] + gp[i];
+          acc_t(dkt[0], sQt[buf][0], dzh, true);
+        } else {
+          acc_t(dk0t, sQt[buf][G], gp, big_tile(gp));
+        }
+      };
+      const bool edge = (qbase < key0 + TILE - 1) || (qbase + TILE > T) || (key0 + TILE > T) || key0 < exempt;
+      if (!SPLIT_BODY || edge) body(std::true_type{});   // the masked body is right on every tile
+      else body(std::false_type{});
     }
     if constexpr (BWD_PIPE) {
       if constexpr (NBUF == 1) __syncthreads();   // the one buffer is free again
@@ -1015,6 +1033,7 @@ __global__ __launch_bounds__(NTHREADS, SA_BWD_MIN_BLOCKS) void bwd_dq_kernel(
   constexpr int LDZ = TILE + OP::KPAD;
   constexpr int AS = OP::acc_steps;
   constexpr int NH = G + 1;
+  constexpr bool SPLIT_BODY = split_body<OP, D>();
   constexpr int TILE_BYTES = (NH * (TILE * LDK + D * LDKT) + G * TILE * LDK) * (int)sizeof(elem);
   constexpr int NBUF = (BWD_PIPE && 2 * TILE_BYTES <= 120 * 1024) ? 2 : 1;
 
@@ -1025,7 +1044,7 @@ __global__ __launch_bounds__(NTHREADS, SA_BWD_MIN_BLOCKS) void bwd_dq_kernel(
   __shared__ __attribute__((aligned(16))) float sLse[NWAVES][G][TILE];
   __shared__ __attribute__((aligned(16))) float sDb[NWAVES][G][TILE];
 
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63, wave = wave_id();
   const int n = lane & 31, h = lane >> 5;
   const int groups = H / G;
   const int b = blockIdx.y / groups, gi = blockIdx.y % groups;
@@ -1170,70 +1189,59 @@ __global__ __launch_bounds__(NTHREADS, SA_BWD_MIN_BLOCKS) void bwd_dq_kernel(
     }
     if (ktile < my_end) {
       const int j = kbase + n;
-      const bool diag = (kbase + TILE - 1 > qbase) || (qbase + TILE > T) || (kbase + TILE > T);
+      auto body = [&](auto edge_tag) {
+        constexpr bool EDGE = decltype(edge_tag)::value;
+        const elem* k0s = has_h0 ? sK[buf][0] : sK[buf][G];
+        f32x16 l0 = zero16();
+#pragma unroll
+        for (int s = 0; s < NS; ++s) l0 = OP::mma(has_h0 ? qa[0][s] : q0a[s], OP::ld_std(k0s, LDK, n, h, s), l0);
+        f32x16 fs, sel;
+        selection_tile<EDGE>(l0, hist * LOG2E, qbase, j, T, exempt, sl2, h, fs, sel);
 
-      const elem* k0s = has_h0 ? sK[buf][0] : sK[buf][G];
-      f32x16 l0 = zero16();
+        f32x16 zsum, dz0;
 #pragma unroll
-      for (int s = 0; s < NS; ++s) l0 = OP::mma(has_h0 ? qa[0][s] : q0a[s], OP::ld_std(k0s, LDK, n, h, s), l0);
-      f32x16 fs;
-      uint32_t gmask;
-      const bool edge = diag || kbase < exempt;
-      selection_tile(l0, hist, qbase, j, T, exempt, scale, h, edge, fs, gmask);
-
-      f32x16 zsum = zero16();
-      f32x16 dz0 = zero16();
+        for (int gg = 0; gg < G; ++gg) {
+          const int g = has_h0 ? (gg + 1) % G : gg;
+          f32x16 lg;
+          if (has_h0 && g == 0) {
+            lg = l0;
+          } else {
+            lg = zero16();
 #pragma unroll
-      for (int gg = 0; gg < G; ++gg) {
-        const int g = has_h0 ? (gg + 1) % G : gg;
-        f32x16 lg;
-        if (has_h0 && g == 0) {
-          lg = l0;
-        } else {
-          lg = zero16();
+            for (int s = 0; s < NS; ++s) lg = OP::mma(qa[g][s], OP::ld_std(sK[buf][g], LDK, n, h, s), lg);
+          }
+          f32x16 dp = zero16();
 #pragma unroll
-          for (int s = 0; s < NS; ++s) lg = OP::mma(qa[g][s], OP::ld_std(sK[buf][g], LDK, n, h, s), lg);
-        }
-        f32x16 dp = zero16();
+          for (int s = 0; s < NS; ++s) dp = OP::mma(doa[g][s], OP::ld_std(sV[buf][g], LDK, n, h, s), dp);
+          f32x16 pr, dz;
+          p_dz_tile<EDGE>(lg, dp, fs, sLse[wave][g], sDb[wave][g], sl2, qbase, j, T, h, pr, dz);
+          if (gg == 0) {
+            zsum = dz;
+          } else {
 #pragma unroll
-        for (int s = 0; s < NS; ++s) dp = OP::mma(doa[g][s], OP::ld_std(sV[buf][g], LDK, n, h, s), dp);
-        f32x16 dz;
-#pragma unroll
-        for (int a = 0; a < 4; ++a) {
-          const float4 ls = *reinterpret_cast<const float4*>(&sLse[wave][g][8 * a + 4 * h]);
-          const float4 dbv = *reinterpret_cast<const float4*>(&sDb[wave][g][8 * a + 4 * h]);
-          const float lsv[4] = {ls.x, ls.y, ls.z, ls.w};
-          const float dbs[4] = {dbv.x, dbv.y, dbv.z, dbv.w};
-#pragma unroll
-          for (int u = 0; u < 4; ++u) {
-            const int i = 4 * a + u;
-            float p = fast_exp2(lg[i] * sl2 - fs[i] - lsv[u]);
-            if (diag) {
-              const int r = qbase + crow(i, h);
-              if (j > r || r >= T || j >= T) p = 0.f;
-            }
-            dz[i] = p * (dp[i] - dbs[u]);
+            for (int i = 0; i < 16; ++i) zsum[i] += dz[i];
+          }
+          if (has_h0 && g == 0) {
+            dz0 = dz;
+          } else {
+            acc_xk(dqacc[g], dz, sKt[buf][g], false);
           }
         }
-#pragma unroll
-        for (int i = 0; i < 16; ++i) zsum[i] += dz[i];
-        if (has_h0 && g == 0) {
-          dz0 = dz;
-        } else {
-          acc_xk(dqacc[g], dz, sKt[buf][g], false);
-        }
-      }
 
-      f32x16 gp;
-      gpath_tile(zsum, uin, gmask, h, gp);
-      if (has_h0) {
-        f32x16 dzh;
+        f32x16 gp;
+        gpath_tile(zsum, uin, sel, h, gp);
+        if (has_h0) {
+          f32x16 dzh;
 #pragma unroll
-        for (int i = 0; i < 16; ++i) dzh[i] = dz0[i] + gp[i];
-        acc_xk(dqacc[0], dzh, sKt[buf][0], true);
-      } else {
-        acc_xk(dq0acc, gp, sKt[buf][G], big_tile(gp));
-      }
+          for (int i = 0; i < 16; ++i) dzh[i] = dz0[i] + gp[i];
+          acc_xk(dqacc[0], dzh, sKt[buf][0], true);
+        } else {
+          acc_xk(dq0acc, gp, sKt[buf][G], big_tile(gp));
+        }
+      };
+      const bool edge = (kbase + TILE - 1 > qbase) || (qbase + TILE > T) || (kbase + TILE > T) || kbase < exempt;
+      if (!SPLIT_BODY || edge) body(std::true_type{});   // the masked body is right on every tile
+      else body(std::false_type{});
     }
     if constexpr (BWD_PIPE) {
       if constexpr (NBUF == 1) __syncthreads();   // the one buffer is free again
