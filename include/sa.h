@@ -15,6 +15,7 @@
  *
  * Tensor layouts (row-major, contiguous):
  *   q, k, v, dout            (nseq*heads, T, D)      storage dtype SA_DTYPE_BF16 or SA_DTYPE_F32
+ *                                                   (sa_forward's k, v: heads kv_stride apart)
  *   out                      (nseq*heads, Tq, D)     fp32
  *   rmax, rden               (nseq*heads, Tq)        fp32   row max (log2 domain) / denominator
  *   carry                    (nseq, ceil(Tq/32), Tk) fp32   per-key selection on entry to every
@@ -87,6 +88,9 @@ int64_t sa_forward_workspace_bytes(int64_t nseq, int64_t heads, int64_t tk, int6
  * before q_offset + tq (for q_offset == 0 it is the reference's `selected_total`,
  * kernels.py:547-549). state_in and state_out may alias.
  *
+ * kv_stride: elements between consecutive heads of k and v (0 = tk * head_dim, the contiguous
+ * layout); a prefill over a preallocated (nseq, heads, capacity, head_dim) cache passes
+ * capacity * head_dim, so no prefix is copied. A multiple of 8.
  * scale: the logit scale s (the reference uses 1/sqrt(D); a caller that zero-pads D passes the
  * unpadded value). group: heads per wavefront (0 = automatic); damp_mode 0 none, 1 linear, 2 sqrt scales F of
  * query i by min(1, train_len/(i+1)) (or its square root), reference kernels.py:179-182.
@@ -96,7 +100,7 @@ int sa_forward(const void* q, const void* k, const void* v,
                const float* state_in, float* state_out, int64_t state_ld,
                void* workspace, int64_t workspace_bytes,
                int64_t nseq, int64_t heads, int64_t tq, int64_t tk, int64_t q_offset,
-               int64_t head_dim, float scale, int dtype, int exempt, int group,
+               int64_t kv_stride, int64_t head_dim, float scale, int dtype, int exempt, int group,
                int damp_mode, int64_t train_len, void* stream);
 
 /* Bytes of scratch sa_backward needs for the same `group` argument (-1 for invalid sizes). */

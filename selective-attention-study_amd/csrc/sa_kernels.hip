@@ -350,7 +350,7 @@ __device__ __forceinline__ float excl_scan32(float x) {
 template <class OP, int D>
 __global__ __launch_bounds__(NTHREADS) void sel_colsum_kernel(
     const typename OP::elem* __restrict__ q, const typename OP::elem* __restrict__ k,
-    float* __restrict__ colsum, int H, int Tq, int Tk, int q_off, int exempt, float scale, int RB) {
+    float* __restrict__ colsum, int H, int Tq, int Tk, int64_t kvs, int q_off, int exempt, float scale, int RB) {
   using elem = typename OP::elem;
   using frag = typename OP::frag;
   constexpr int NS = D / OP::KS;
@@ -362,7 +362,7 @@ __global__ __launch_bounds__(NTHREADS) void sel_colsum_kernel(
   if (kb >= NKT) return;
   const int b = blockIdx.z;
   const elem* q0 = q + (int64_t)b * H * Tq * D;
-  const elem* k0 = k + (int64_t)b * H * Tk * D;
+  const elem* k0 = k + (int64_t)b * H * kvs;
   const int j = kb * TILE + n;
 
   frag kf[NS];
@@ -418,7 +418,7 @@ __global__ __launch_bounds__(NTHREADS) void fwd_kernel(
     const typename OP::elem* __restrict__ q, const typename OP::elem* __restrict__ k,
     const typename OP::elem* __restrict__ vt, const float* __restrict__ carry,
     float* __restrict__ out, float* __restrict__ rmax, float* __restrict__ rden,
-    int H, int Tq, int Tk, int q_off, int64_t ldv, int exempt, float scale,
+    int H, int Tq, int Tk, int64_t kvs, int q_off, int64_t ldv, int exempt, float scale,
     int damp_mode, float train_len) {
   using elem = typename OP::elem;
   using frag = typename OP::frag;
@@ -490,10 +490,10 @@ __global__ __launch_bounds__(NTHREADS) void fwd_kernel(
     __syncthreads();
 #pragma unroll
     for (int g = 0; g < G; ++g) {
-      stage_rows<elem, D, LDK>(sK[g], k + (seq_row + hd0 + g) * Tk * D, D, kbase, Tk, tid);
+      stage_rows<elem, D, LDK>(sK[g], k + (seq_row + hd0 + g) * kvs, D, kbase, Tk, tid);
       stage_cols<elem, D, LDV>(sVt[g], vt + (seq_row + hd0 + g) * D * ldv, ldv, kbase, Tk, tid);
     }
-    if (!has_h0) stage_rows<elem, D, LDK>(sK[G], k + seq_row * Tk * D, D, kbase, Tk, tid);
+    if (!has_h0) stage_rows<elem, D, LDK>(sK[G], k + seq_row * kvs, D, kbase, Tk, tid);
     __syncthreads();
     if (kt >= my_end) continue;
 
@@ -608,11 +608,11 @@ __global__ __launch_bounds__(NTHREADS) void bwd_rowstats_kernel(
 // in (R, T, D) -> outT (R, D, ldt); a workgroup moves a [64 t][D] slab through LDS.
 template <typename E, int D>
 __global__ __launch_bounds__(NTHREADS) void transpose_kernel(const E* __restrict__ in, E* __restrict__ outT,
-                                                             int T, int64_t ldt) {
+                                                             int T, int64_t ldt, int64_t in_stride) {
   __shared__ E tile[64][D + 1];
   const int64_t r = blockIdx.y;
   const int t0 = blockIdx.x * 64;
-  const E* src = in + r * T * D;
+  const E* src = in + r * in_stride;
   for (int c = threadIdx.x; c < 64 * D; c += NTHREADS) {
     const int tt = c / D, d = c % D;
     tile[tt][d] = (t0 + tt < T) ? src[(int64_t)(t0 + tt) * D + d] : (E)0;
@@ -1364,14 +1364,14 @@ int auto_group(int dtype, int64_t D, int64_t heads, int requested, bool backward
 
 template <class OP, int D>
 int run_selection(const typename OP::elem* q, const typename OP::elem* k, float* carry, const float* state_in,
-                  float* state_out, int64_t state_ld, int nseq, int H, int Tq, int Tk, int q_off, int exempt,
-                  float scale, hipStream_t st) {
+                  float* state_out, int64_t state_ld, int nseq, int H, int Tq, int Tk, int64_t kvs, int q_off,
+                  int exempt, float scale, hipStream_t st) {
   const int NBq = (int)cdiv(Tq, TILE), NKT = (int)cdiv(Tk, TILE);
   const int RB = 8;
   dim3 g1((unsigned)cdiv(NKT, NWAVES), (unsigned)cdiv(NBq, RB), (unsigned)nseq);
   TimedLaunch timed(SA_KERNEL_SELECTION, st);
-  hipLaunchKernelGGL((sel_colsum_kernel<OP, D>), g1, dim3(NTHREADS), 0, st, q, k, carry, H, Tq, Tk, q_off, exempt,
-                     scale, RB);
+  hipLaunchKernelGGL((sel_colsum_kernel<OP, D>), g1, dim3(NTHREADS), 0, st, q, k, carry, H, Tq, Tk, kvs, q_off,
+                     exempt, scale, RB);
   dim3 g2((unsigned)cdiv(Tk, NTHREADS), (unsigned)nseq);
   hipLaunchKernelGGL(sel_scan_kernel, g2, dim3(NTHREADS), 0, st, carry, state_in, state_out, state_ld, NBq, Tk,
                      q_off);
@@ -1381,18 +1381,19 @@ int run_selection(const typename OP::elem* q, const typename OP::elem* k, float*
 template <class OP, int D, int G>
 void launch_fwd(const typename OP::elem* q, const typename OP::elem* k, const typename OP::elem* vt,
                 const float* carry, float* out, float* rmax, float* rden, int nseq, int H, int Tq, int Tk,
-                int q_off, int64_t ldv, int exempt, float scale, int damp_mode, float train_len, hipStream_t st) {
+                int64_t kvs, int q_off, int64_t ldv, int exempt, float scale, int damp_mode, float train_len,
+                hipStream_t st) {
   const int NBq = (int)cdiv(Tq, TILE);
   dim3 grid((unsigned)cdiv(NBq, NWAVES), (unsigned)(nseq * (H / G)));
   TimedLaunch timed(SA_KERNEL_FORWARD, st);
   hipLaunchKernelGGL((fwd_kernel<OP, D, G>), grid, dim3(NTHREADS), 0, st, q, k, vt, carry, out, rmax, rden, H, Tq,
-                     Tk, q_off, ldv, exempt, scale, damp_mode, train_len);
+                     Tk, kvs, q_off, ldv, exempt, scale, damp_mode, train_len);
 }
 
 template <class OP, int D>
 int forward_impl(const void* q_, const void* k_, const void* v_, float* out, float* rmax, float* rden,
                  float* carry, const float* state_in, float* state_out, int64_t state_ld, void* ws, int nseq,
-                 int H, int Tq, int Tk, int q_off, float scale, int exempt, int group, int damp_mode,
+                 int H, int Tq, int Tk, int64_t kvs, int q_off, float scale, int exempt, int group, int damp_mode,
                  float train_len, hipStream_t st) {
   using elem = typename OP::elem;
   const elem* q = static_cast<const elem*>(q_);
@@ -1401,21 +1402,22 @@ int forward_impl(const void* q_, const void* k_, const void* v_, float* out, flo
   const int64_t ldv = sa_transposed_ld(Tk);
   elem* vt = static_cast<elem*>(ws);
   dim3 gt((unsigned)cdiv(ldv, 64), (unsigned)(nseq * H));
-  hipLaunchKernelGGL((transpose_kernel<elem, D>), gt, dim3(NTHREADS), 0, st, v, vt, Tk, ldv);
-  int rc = run_selection<OP, D>(q, k, carry, state_in, state_out, state_ld, nseq, H, Tq, Tk, q_off, exempt, scale, st);
+  hipLaunchKernelGGL((transpose_kernel<elem, D>), gt, dim3(NTHREADS), 0, st, v, vt, Tk, ldv, kvs);
+  int rc = run_selection<OP, D>(q, k, carry, state_in, state_out, state_ld, nseq, H, Tq, Tk, kvs, q_off, exempt,
+                                scale, st);
   if (rc) return rc;
   const int dtype = sizeof(elem) == 2 ? SA_DTYPE_BF16 : SA_DTYPE_F32;
   const int G = auto_group(dtype, D, H, group, false);
   if (G == 4) {
     if constexpr (sizeof(elem) == 2 && D <= 64)
-      launch_fwd<OP, D, 4>(q, k, vt, carry, out, rmax, rden, nseq, H, Tq, Tk, q_off, ldv, exempt, scale, damp_mode,
+      launch_fwd<OP, D, 4>(q, k, vt, carry, out, rmax, rden, nseq, H, Tq, Tk, kvs, q_off, ldv, exempt, scale, damp_mode,
                            train_len, st);
   } else if (G == 2) {
     if constexpr (sizeof(elem) == 2 && D <= 64)
-      launch_fwd<OP, D, 2>(q, k, vt, carry, out, rmax, rden, nseq, H, Tq, Tk, q_off, ldv, exempt, scale, damp_mode,
+      launch_fwd<OP, D, 2>(q, k, vt, carry, out, rmax, rden, nseq, H, Tq, Tk, kvs, q_off, ldv, exempt, scale, damp_mode,
                            train_len, st);
   } else {
-    launch_fwd<OP, D, 1>(q, k, vt, carry, out, rmax, rden, nseq, H, Tq, Tk, q_off, ldv, exempt, scale, damp_mode,
+    launch_fwd<OP, D, 1>(q, k, vt, carry, out, rmax, rden, nseq, H, Tq, Tk, kvs, q_off, ldv, exempt, scale, damp_mode,
                          train_len, st);
   }
   return launch_status();
@@ -1507,9 +1509,9 @@ int backward_impl(const void* q_, const void* k_, const void* v_, const float* o
   float* ucheck = reinterpret_cast<float*>(base + L.ucheck);
 
   dim3 gt((unsigned)cdiv(ldt, 64), (unsigned)R);
-  hipLaunchKernelGGL((transpose_kernel<elem, D>), gt, dim3(NTHREADS), 0, st, q, qt, T, ldt);
-  hipLaunchKernelGGL((transpose_kernel<elem, D>), gt, dim3(NTHREADS), 0, st, dout, dot, T, ldt);
-  hipLaunchKernelGGL((transpose_kernel<elem, D>), gt, dim3(NTHREADS), 0, st, k, kt, T, ldt);
+  hipLaunchKernelGGL((transpose_kernel<elem, D>), gt, dim3(NTHREADS), 0, st, q, qt, T, ldt, (int64_t)T * D);
+  hipLaunchKernelGGL((transpose_kernel<elem, D>), gt, dim3(NTHREADS), 0, st, dout, dot, T, ldt, (int64_t)T * D);
+  hipLaunchKernelGGL((transpose_kernel<elem, D>), gt, dim3(NTHREADS), 0, st, k, kt, T, ldt, (int64_t)T * D);
   hipLaunchKernelGGL((bwd_rowstats_kernel<OP, D>), dim3((unsigned)cdiv(R * T, NTHREADS)), dim3(NTHREADS), 0, st,
                      dout, out, rmax, rden, lse, dbar, R * T);
   // head 0's shares from the other groups are atomic targets (one add per element and group)
@@ -1606,9 +1608,11 @@ int64_t sa_forward_workspace_bytes(int64_t nseq, int64_t heads, int64_t tk, int6
 int sa_forward(const void* q, const void* k, const void* v, float* out, float* rmax, float* rden, float* carry,
                const float* state_in, float* state_out, int64_t state_ld, void* workspace,
                int64_t workspace_bytes, int64_t nseq, int64_t heads, int64_t tq, int64_t tk, int64_t q_offset,
-               int64_t head_dim, float scale, int dtype, int exempt, int group, int damp_mode, int64_t train_len,
-               void* stream) {
+               int64_t kv_stride, int64_t head_dim, float scale, int dtype, int exempt, int group, int damp_mode,
+               int64_t train_len, void* stream) {
   if (!valid_dims(nseq, heads, tk) || tq < 1 || q_offset < 0 || q_offset + tq != tk) return SA_ERR_ARGUMENT;
+  if (kv_stride == 0) kv_stride = tk * head_dim;
+  if (kv_stride < tk * head_dim || kv_stride % 8 != 0) return SA_ERR_ARGUMENT;
   if (!q || !k || !v || !out || !rmax || !rden || !carry || !state_out || !workspace) return SA_ERR_ARGUMENT;
   if (q_offset > 0 && !state_in) return SA_ERR_ARGUMENT;
   if (state_ld < tk || exempt < 1 || damp_mode < 0 || damp_mode > 2 || (damp_mode && train_len < 1))
@@ -1622,7 +1626,7 @@ int sa_forward(const void* q, const void* k, const void* v, float* out, float* r
   const float tl = (float)train_len;
 #define SA_FWD(OPT, DD)                                                                                             \
   return forward_impl<OPT, DD>(q, k, v, out, rmax, rden, carry, state_in, state_out, state_ld, workspace, ns, H, Tq, \
-                               Tk, qo, scale, exempt, group, damp_mode, tl, st)
+                               Tk, kv_stride, qo, scale, exempt, group, damp_mode, tl, st)
   if (dtype == SA_DTYPE_BF16) {
     if (head_dim == 32) SA_FWD(OpBF16, 32);
     if (head_dim == 64) SA_FWD(OpBF16, 64);

@@ -1,0 +1,183 @@
+"""Measurements of the operator inside a model, for BASELINE's configurations beyond the single-layer
+fwd+bwd (bench.py measures that one):
+
+    C3  train_step_rate    one training step of the 24-layer decoder at 1 x 16384 tokens, bf16
+                           autocast, fused AdamW (reference train.py:624-650, runtime.py:610-638)
+    C4  prefill_rate       forward-only prefill of 131072 tokens in chunks of 16384, every layer
+                           carrying its K/V and per-key selection state between chunks
+    C5  perhead_rate       per-head selection fwd+bwd at B=2, H=16, T=32768, D=64 with k scaled by 2
+                           on a random 10% of key positions
+
+Synthetic inputs only: token ids uniform over the GPT-2 vocabulary with <BOS> (50256) first, the
+reference's window rule input = [bos] + window[:-1], targets = window (data.py:136-139);
+random-init weights. Times are HIP events around whole steps after warm-up.
+
+    python -m selective_attention.harness c3 [--geometry d768|d1024] [--steps K] [--warmup W]
+    python -m selective_attention.harness c4 [--tokens 131072] [--chunk 16384]
+    python -m selective_attention.harness c5
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import sys
+
+import torch
+
+from . import kernels
+from .model import ModelConfig, SelectiveLM
+
+GPT2_VOCAB = 50257
+BOS = 50256
+GEOMETRIES = {
+    "d768": dict(d_model=768, n_heads=12),     # the reference's 209M model (configs/scale_16384/*.yaml)
+    "d1024": dict(d_model=1024, n_heads=16),   # BASELINE's literal geometry (353.5M parameters)
+}
+PEAK_BF16_TFLOPS = 2500.0
+
+
+def synthetic_batch(batch: int, seq: int, device, seed: int = 0) -> tuple[torch.Tensor, torch.Tensor]:
+    """(input ids, targets): a uniform random window with <BOS> prepended to the inputs."""
+    g = torch.Generator(device="cpu").manual_seed(seed)
+    window = torch.randint(0, GPT2_VOCAB, (batch, seq), generator=g)
+    idx = torch.cat([torch.full_like(window[:, :1], BOS), window[:, :-1]], dim=1)
+    return idx.to(device), window.to(device)
+
+
+def _timed(fn, steps: int, warmup: int) -> float:
+    """Milliseconds per call of fn(), HIP events around `steps` calls after `warmup` calls."""
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record()
+    for _ in range(steps):
+        fn()
+    stop.record()
+    torch.cuda.synchronize()
+    return start.elapsed_time(stop) / steps
+
+
+def model_flop_per_token(cfg: ModelConfig, seq: int) -> float:
+    """Training FLOP per token: 6 N (dense) + the attention products, 7 H D T per layer under the
+    FlashAttention convention (causal pairs T^2/2 counted once, backward 2.5 x forward)."""
+    n = sum(p for p in _param_counts(cfg))
+    hd = cfg.d_model // cfg.n_heads
+    return 6.0 * n + cfg.n_layers * 7.0 * cfg.n_heads * hd * seq
+
+
+def _param_counts(cfg: ModelConfig):
+    with torch.device("meta"):
+        m = SelectiveLM(cfg)
+    yield sum(p.numel() for name, p in m.named_parameters() if "wte" not in name)
+
+
+def train_step_rate(geometry: str = "d768", steps: int = 10, warmup: int = 3, seq: int = 16384, batch: int = 1,
+                    layers: int = 24) -> dict:
+    """C3: tokens per second of full training steps (forward, backward, grad clip, fused AdamW)."""
+    dev = torch.device("cuda")
+    cfg = ModelConfig(n_layers=layers, context_length=seq, **GEOMETRIES[geometry])
+    torch.manual_seed(0)
+    model = SelectiveLM(cfg).to(dev).train()
+    opt = torch.optim.AdamW(model.parameters(), lr=6e-4, betas=(0.9, 0.95), eps=1e-8, weight_decay=0.1, fused=True)
+    idx, targets = synthetic_batch(batch, seq, dev)
+    losses = []
+
+    def step():
+        with torch.autocast("cuda", dtype=torch.bfloat16):
+            _, loss = model(idx, targets)
+        loss.backward()
+        torch.nn.utils.clip_grad_norm_(model.parameters(), 1.0)
+        opt.step()
+        opt.zero_grad(set_to_none=True)
+        losses.append(loss.detach())
+
+    torch.cuda.reset_peak_memory_stats()
+    ms = _timed(step, steps, warmup)
+    final = float(losses[-1])
+    if not math.isfinite(final):
+        raise RuntimeError(f"non-finite training loss {final}")
+    tokens = batch * seq
+    flop = model_flop_per_token(cfg, seq) * tokens
+    return {"config": f"C3 train step, {geometry} ({model.num_parameters()} params), {layers} layers, "
+                      f"{batch}x{seq} tokens, bf16 autocast, fused AdamW, eager",
+            "tokens_per_s": tokens / (ms * 1e-3), "ms_per_step": ms, "model_tflops": flop / (ms * 1e-3) / 1e12,
+            "loss": final, "peak_mem_gib": torch.cuda.max_memory_allocated() / 2**30, "steps": steps,
+            "warmup": warmup}
+
+
+def prefill_rate(tokens: int = 131072, chunk: int = 16384, geometry: str = "d1024", layers: int = 24,
+                 reps: int = 1, warmup: int = 1) -> dict:
+    """C4: tokens per second of a chunked prefill (forward only, bf16 weights)."""
+    dev = torch.device("cuda")
+    cfg = ModelConfig(n_layers=layers, context_length=tokens, **GEOMETRIES[geometry])
+    torch.manual_seed(0)
+    model = SelectiveLM(cfg).to(dev, torch.bfloat16).eval()
+    idx, _ = synthetic_batch(1, tokens, dev, seed=1)
+
+    def run():
+        with torch.no_grad():
+            model.prefill_chunked(idx, chunk)
+
+    torch.cuda.reset_peak_memory_stats()
+    ms = _timed(run, reps, warmup)
+    hd = cfg.d_model // cfg.n_heads
+    attn_flop = layers * 2.0 * cfg.n_heads * hd * tokens * tokens
+    return {"config": f"C4 prefill, {geometry}, {layers} layers, {tokens} tokens in chunks of {chunk}, bf16",
+            "tokens_per_s": tokens / (ms * 1e-3), "ms": ms, "attention_tflops": attn_flop / (ms * 1e-3) / 1e12,
+            "peak_mem_gib": torch.cuda.max_memory_allocated() / 2**30}
+
+
+def perhead_rate(batch: int = 2, heads: int = 16, seq: int = 32768, head_dim: int = 64, steps: int = 5,
+                 warmup: int = 2) -> dict:
+    """C5: per-head selection fwd+bwd TFLOP/s; each head is its own one-head sequence, keys of a
+    random 10% of positions scaled by 2."""
+    dev = torch.device("cuda")
+    g = torch.Generator(device=dev).manual_seed(5)
+    q, k, v, do = (torch.randn(batch, heads, seq, head_dim, device=dev, generator=g) for _ in range(4))
+    boost = torch.rand(batch, heads, seq, 1, device=dev, generator=g) < 0.1
+    k = torch.where(boost, 2.0 * k, k)
+    r = lambda t: t.reshape(batch * heads, 1, seq, head_dim)
+    qq, kk, vv = (r(t).bfloat16().requires_grad_(True) for t in (q, k, v))
+    dd = r(do)
+
+    def step():
+        out = kernels.selective_attention(qq, kk, vv)
+        torch.autograd.grad(out, (qq, kk, vv), dd)
+
+    ms = _timed(step, steps, warmup)
+    flop = 7.0 * batch * heads * head_dim * seq * seq
+    tf = flop / (ms * 1e-3) / 1e12
+    return {"config": f"C5 per-head fwd+bwd, B={batch} H={heads} T={seq} D={head_dim} bf16, k x2 on 10% of keys",
+            "ms_per_step": ms, "tflops": tf, "frac_of_peak": tf / PEAK_BF16_TFLOPS}
+
+
+def main(argv=None) -> int:
+    ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
+    ap.add_argument("which", choices=["c3", "c4", "c5"])
+    ap.add_argument("--geometry", default=None, choices=sorted(GEOMETRIES))
+    ap.add_argument("--steps", type=int, default=None)
+    ap.add_argument("--warmup", type=int, default=None)
+    ap.add_argument("--layers", type=int, default=24)
+    ap.add_argument("--tokens", type=int, default=131072)
+    ap.add_argument("--chunk", type=int, default=16384)
+    a = ap.parse_args(argv)
+    if not torch.cuda.is_available():
+        print("needs a ROCm GPU", file=sys.stderr)
+        return 2
+    kw = {k: v for k, v in (("steps", a.steps), ("warmup", a.warmup)) if v is not None}
+    if a.which == "c3":
+        res = train_step_rate(a.geometry or "d768", layers=a.layers, **kw)
+    elif a.which == "c4":
+        res = prefill_rate(a.tokens, a.chunk, a.geometry or "d1024", a.layers,
+                           **({"reps": a.steps} if a.steps else {}), **({"warmup": a.warmup} if a.warmup is not None else {}))
+    else:
+        res = perhead_rate(**kw)
+    print(json.dumps(res), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

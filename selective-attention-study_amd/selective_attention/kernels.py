@@ -171,11 +171,33 @@ def _storage(t: torch.Tensor, n: int, dtype: int, kdim: int) -> torch.Tensor:
     return x.contiguous()
 
 
+def _kv_storage(t: torch.Tensor, n: int, dtype: int, kdim: int, allow_view: bool) -> tuple[torch.Tensor, int]:
+    """(B, H, T, D) keys or values for sa_forward, and the element stride between heads. A view whose
+    heads sit a fixed stride apart with contiguous (T, D) rows inside each head (a slice of a
+    preallocated cache) is passed as is; anything else becomes contiguous first."""
+
+    want = torch.bfloat16 if dtype == _lib.DTYPE_BF16 else torch.float32
+    batch, heads, seq, head_dim = t.shape
+    if allow_view and t.dtype == want and head_dim == kdim and t.stride(3) == 1 and t.stride(2) == head_dim:
+        # flattened row r = b * heads + h must start at r * hs
+        if heads > 1:
+            hs = t.stride(1)
+            rows_ok = batch == 1 or t.stride(0) == heads * hs
+        else:
+            hs = t.stride(0) if batch > 1 else seq * head_dim
+            rows_ok = True
+        if rows_ok and hs >= seq * head_dim and hs % 8 == 0 and t.data_ptr() % 16 == 0:
+            return t, hs
+    x = _storage(t, n, dtype, kdim)
+    return x, seq * kdim
+
+
 def _stream(device: torch.device) -> int:
     return torch.cuda.current_stream(device).cuda_stream
 
 
-def _forward_launch(q, k, v, dtype, exempt, group, damp_mode, train_len, state_in=None, q_offset=0, state=None):
+def _forward_launch(q, k, v, dtype, exempt, group, damp_mode, train_len, state_in=None, q_offset=0, state=None,
+                    allow_view=True):
     """Run sa_forward on (B, H, Tq, D) q and (B, H, Tk, D) k, v; returns the padded fp32 output
     (B*H, Tq, kdim), rmax, rden, carry, the storage tensors and the state."""
 
@@ -186,8 +208,11 @@ def _forward_launch(q, k, v, dtype, exempt, group, damp_mode, train_len, state_i
     kdim = _kernel_dim(head_dim)
     dev = q.device
     qs = _storage(q, n, dtype, kdim)
-    ks = _storage(k, n, dtype, kdim)
-    vs = _storage(v, n, dtype, kdim)
+    ks, kstride = _kv_storage(k, n, dtype, kdim, allow_view)
+    vs, vstride = _kv_storage(v, n, dtype, kdim, allow_view)
+    if kstride != vstride:   # one stride serves both: fall back to contiguous copies
+        ks, vs = _storage(k, n, dtype, kdim), _storage(v, n, dtype, kdim)
+        kstride = tk * kdim
     nb = (tq + CARRY_M - 1) // CARRY_M
     out = torch.empty(n, tq, kdim, device=dev, dtype=torch.float32)
     rmax = torch.empty(n, tq, device=dev, dtype=torch.float32)
@@ -201,7 +226,7 @@ def _forward_launch(q, k, v, dtype, exempt, group, damp_mode, train_len, state_i
         _lib.check(lib.sa_forward(
             qs.data_ptr(), ks.data_ptr(), vs.data_ptr(), out.data_ptr(), rmax.data_ptr(), rden.data_ptr(),
             carry.data_ptr(), None if state_in is None else state_in.data_ptr(), state.data_ptr(),
-            state.stride(0), ws.data_ptr(), ws.numel(), batch, heads, tq, tk, q_offset, kdim,
+            state.stride(0), ws.data_ptr(), ws.numel(), batch, heads, tq, tk, q_offset, kstride, kdim,
             1.0 / math.sqrt(head_dim), dtype, exempt, group, damp_mode, train_len, _stream(dev)))
     return out, rmax, rden, carry, state, (qs, ks, vs)
 
@@ -300,7 +325,7 @@ class _SelectiveAttentionFn(torch.autograd.Function):
         _check_blocks(block_m, block_n)
         batch, heads, seq, head_dim = q.shape
         out, rmax, rden, carry, _, (qs, ks, vs) = _forward_launch(
-            q, k, v, dtype, exempt, int(group or 0), 0, 0)
+            q, k, v, dtype, exempt, int(group or 0), 0, 0, allow_view=False)
         ctx.save_for_backward(qs, ks, vs, out, rmax, rden, carry)
         ctx.meta = (dtype, exempt, bwd_group, head_dim, (q.dtype, k.dtype, v.dtype), batch, heads)
         result = out[..., :head_dim].reshape(batch, heads, seq, head_dim)

@@ -53,21 +53,24 @@ def test_invalid_arguments_are_rejected_before_any_launch():
     """Host validation in C: no pointer is dereferenced, no kernel launched."""
     lib = _lib.load()
     fake = 1 << 20   # never dereferenced: validation fails first
-    args = [fake] * 9 + [16, fake, 1 << 30, 1, 4, 16, 16, 0, 64, 0.125, 0, 1, 0, 0, 0, None]
+    args = [fake] * 9 + [16, fake, 1 << 30, 1, 4, 16, 16, 0, 0, 64, 0.125, 0, 1, 0, 0, 0, None]
     bad = list(args)
     bad[16] = 5          # q_offset + tq != tk
     assert lib.sa_forward(*bad) == -1
     bad = list(args)
-    bad[17] = 48         # head_dim
+    bad[18] = 48         # head_dim
     assert lib.sa_forward(*bad) == -2
     bad = list(args)
-    bad[19] = 7          # dtype
+    bad[17] = 16 * 64 - 8   # kv_stride below tk * head_dim
+    assert lib.sa_forward(*bad) == -1
+    bad = list(args)
+    bad[20] = 7          # dtype
     assert lib.sa_forward(*bad) == -3
     bad = list(args)
     bad[11] = 16         # workspace too small
     assert lib.sa_forward(*bad) == -4
     bad = list(args)
-    bad[20] = 0          # exempt
+    bad[21] = 0          # exempt
     assert lib.sa_forward(*bad) == -1
     bargs = [fake] * 12 + [1 << 30, 1, 4, 16, 64, 0.125, 0, 1, 1, 0, None]
     bad = list(bargs)

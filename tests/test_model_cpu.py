@@ -1,0 +1,109 @@
+"""The decoder harness and the SelectiveAttention slot on the CPU (reference tests/test_selective_model.py,
+tests/test_selective_perhead.py). The layers run the plain listing here (use_kernel = False, the
+explicit opt-in); the kernel path of the same layers is tested on the GPU (test_model_gpu.py)."""
+
+from __future__ import annotations
+
+import pytest
+import torch
+
+from oracle import sa_oracle
+from selective_attention import mixers
+from selective_attention.model import ATTENTION_TYPES, ModelConfig, SelectiveLM, attention_classes
+
+
+def _tiny(attention="selective", layers=2, **kw):
+    cfg = ModelConfig(vocab_size=97, n_layers=layers, d_model=64, n_heads=4, context_length=64, attention=attention,
+                      **kw)
+    torch.manual_seed(0)
+    model = SelectiveLM(cfg).double()
+    for block in model.transformer.h:
+        block.attn.use_kernel = False
+    return model.eval()
+
+
+def test_registry_names_match_the_reference():
+    """reference mixers.py:21-32, tests/test_selective_model.py:24-27"""
+    assert mixers.MIXER_TYPES == ("selective", "selective_x16", "selective_perhead")
+    assert set(attention_classes()) == {"softmax", *mixers.MIXER_TYPES}
+    assert set(ATTENTION_TYPES) == set(attention_classes())
+    with pytest.raises(ValueError, match="unknown attention"):
+        ModelConfig(attention="dilution")
+
+
+def test_parameter_counts():
+    """208,540,416 is the reference run record's count for its 16K model
+    (runs/scale_16384/all_selective_nope_bos_seed1337/metrics.jsonl:1); d1024/16H is BASELINE's
+    literal geometry. Selective attention adds no parameters over softmax attention."""
+    with torch.device("meta"):
+        assert SelectiveLM(ModelConfig()).num_parameters() == 208_540_416
+        assert SelectiveLM(ModelConfig(d_model=1024, n_heads=16)).num_parameters() == 353_502_208
+        assert (SelectiveLM(ModelConfig(n_layers=2)).num_parameters()
+                == SelectiveLM(ModelConfig(n_layers=2, attention="softmax")).num_parameters())
+
+
+def test_state_dict_names_follow_the_reference():
+    keys = set(SelectiveLM(ModelConfig(n_layers=1, d_model=64, n_heads=4, vocab_size=50)).state_dict())
+    assert keys == {"transformer.wte.weight", "lm_head.weight", "transformer.ln_f.weight",
+                    "transformer.h.0.ln_1.weight", "transformer.h.0.ln_2.weight",
+                    "transformer.h.0.attn.c_attn.weight", "transformer.h.0.attn.c_proj.weight",
+                    "transformer.h.0.mlp.gate_proj.weight", "transformer.h.0.mlp.up_proj.weight",
+                    "transformer.h.0.mlp.down_proj.weight"}
+
+
+def test_layer_matches_the_oracle():
+    """One SelectiveAttention layer == projections around oracle.attention."""
+    model = _tiny()
+    layer = model.transformer.h[0].attn
+    x = torch.randn(2, 30, 64, dtype=torch.float64)
+    q, k, v = layer._split_heads(x)
+    want = layer._merge_heads(sa_oracle.attention(q, k, v), 2, 30)
+    torch.testing.assert_close(layer(x), want)
+
+
+@pytest.mark.parametrize("attention", ["selective", "selective_x16", "selective_perhead"])
+def test_cached_decode_equals_full_forward(attention):
+    """Prefill then decode steps give the full forward's logits (reference
+    tests/test_selective_model.py:42-53, test_selective_perhead.py:32-51)."""
+    model = _tiny(attention)
+    idx = torch.randint(0, 97, (2, 40))
+    with torch.no_grad():
+        full = model.transformer.ln_f(_hidden(model, idx))
+        full_logits = model.lm_head(full)
+        logits, caches = model.prefill(idx[:, :25], capacity=40)
+        torch.testing.assert_close(logits[:, 0], full_logits[:, 24])
+        for t in range(25, 40):
+            step = model.decode_step(idx[:, t:t + 1], t, caches)
+            torch.testing.assert_close(step[:, 0], full_logits[:, t])
+
+
+def _hidden(model, idx):
+    x = model.transformer.wte(idx)
+    for block in model.transformer.h:
+        x = block(x)
+    return x
+
+
+def test_per_head_layer_is_each_head_alone():
+    """selective_perhead == every head as its own one-head sequence (reference mixers.py:76-84)."""
+    model = _tiny("selective_perhead")
+    layer = model.transformer.h[0].attn
+    x = torch.randn(1, 20, 64, dtype=torch.float64)
+    q, k, v = layer._split_heads(x)
+    torch.testing.assert_close(layer._attend(q, k, v)[0], sa_oracle.per_head(q, k, v))
+
+
+def test_kernel_layers_refuse_cpu_tensors():
+    """No silent fallback: with use_kernel on, a CPU input is an error, not the listing."""
+    model = _tiny()
+    model.transformer.h[0].attn.use_kernel = True
+    with pytest.raises((ValueError, RuntimeError)):
+        model(torch.randint(0, 97, (1, 8)))
+
+
+def test_training_loss_and_backward_on_cpu_listing():
+    model = _tiny().train()
+    idx = torch.randint(0, 97, (2, 33))
+    _, loss = model(idx[:, :-1], idx[:, 1:])
+    loss.backward()
+    assert torch.isfinite(loss) and all(torch.isfinite(p.grad).all() for p in model.parameters())
