@@ -12,7 +12,10 @@ forward + backward 7*B*H*D*T^2, causal pairs counted as T^2/2), the roofline of 
 / its average HIP-event duration inside the timed region, against the 2.5 PFLOP/s dense bf16 MFMA peak), and a CPU baseline: the fp32 listing (the
 test oracle) timed on this host for a bounded sample of the same workload.
 
-    python bench.py [--steps K] [--warmup W] [--no-cpu-baseline]
+The same line carries the metric's "train tok/s": full training steps of the 24-layer decoder at
+1 x 16384 tokens (the reference's 209M geometry; selective_attention/harness.py, config C3).
+
+    python bench.py [--steps K] [--warmup W] [--no-cpu-baseline] [--no-train]
 """
 
 from __future__ import annotations
@@ -93,6 +96,7 @@ def main() -> int:
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-train", action="store_true", help="skip the 24-layer training-step rate (C3)")
     args = ap.parse_args()
     if args.gpus != 1:
         print("bench.py measures one GPU only: the operator runs on a single MI355X "
@@ -163,6 +167,15 @@ def main() -> int:
                      "achieved": round(achieved, 2), "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
                      "frac": round(achieved / PEAK_BF16_TFLOPS, 4), "traffic": None},
     }
+    if not args.no_train:
+        # the metric's "train tok/s": C3, the reference's 209M geometry (d768, 12 heads x 64, 24 layers)
+        del q, k, v, do, grads
+        torch.cuda.empty_cache()
+        from selective_attention import harness
+
+        tr = harness.train_step_rate("d768", steps=5, warmup=2)
+        record["train_tok_s"] = round(tr["tokens_per_s"], 1)
+        record["train"] = {k_: (round(v_, 3) if isinstance(v_, float) else v_) for k_, v_ in tr.items()}
     if not args.no_cpu_baseline:
         record["cpu_baseline"] = cpu_baseline()
     print(json.dumps(record), flush=True)

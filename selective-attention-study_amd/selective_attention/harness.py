@@ -15,6 +15,7 @@ random-init weights. Times are HIP events around whole steps after warm-up.
     python -m selective_attention.harness c3 [--geometry d768|d1024] [--steps K] [--warmup W]
     python -m selective_attention.harness c4 [--tokens 131072] [--chunk 16384]
     python -m selective_attention.harness c5
+    python -m selective_attention.harness copy      (reference copy for rocprofv3 byte counters)
 """
 
 from __future__ import annotations
@@ -154,9 +155,19 @@ def perhead_rate(batch: int = 2, heads: int = 16, seq: int = 32768, head_dim: in
             "ms_per_step": ms, "tflops": tf, "frac_of_peak": tf / PEAK_BF16_TFLOPS}
 
 
+def copy_probe(mib: int = 1024, reps: int = 3) -> dict:
+    """A plain device-to-device copy of `mib` MiB, `reps` times: the reference point that scales the
+    FETCH_SIZE / WRITE_SIZE counters of rocprofv3 (each copy reads and writes exactly `mib` MiB)."""
+    dev = torch.device("cuda")
+    src = torch.ones(mib * 2**20 // 4, device=dev)
+    dst = torch.empty_like(src)
+    ms = _timed(lambda: dst.copy_(src), reps, 1)
+    return {"config": f"copy of {mib} MiB", "ms": ms, "gb_per_s": 2 * mib * 2**20 / (ms * 1e-3) / 1e9}
+
+
 def main(argv=None) -> int:
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
-    ap.add_argument("which", choices=["c3", "c4", "c5"])
+    ap.add_argument("which", choices=["c3", "c4", "c5", "copy"])
     ap.add_argument("--geometry", default=None, choices=sorted(GEOMETRIES))
     ap.add_argument("--steps", type=int, default=None)
     ap.add_argument("--warmup", type=int, default=None)
@@ -173,8 +184,10 @@ def main(argv=None) -> int:
     elif a.which == "c4":
         res = prefill_rate(a.tokens, a.chunk, a.geometry or "d1024", a.layers,
                            **({"reps": a.steps} if a.steps else {}), **({"warmup": a.warmup} if a.warmup is not None else {}))
-    else:
+    elif a.which == "c5":
         res = perhead_rate(**kw)
+    else:
+        res = copy_probe()
     print(json.dumps(res), flush=True)
     return 0
 
