@@ -348,3 +348,45 @@ def test_c2_full_length_prefix_is_exact(cuda):
     assert (got - want).abs().max().item() < 2e-2
     rel = (aux["selected_total"].cpu() - total).abs().max() / total.abs().max()
     assert rel.item() < 1e-2
+
+
+def test_c1_fp32_forward_within_1e_4_relative(cuda):
+    """C1: B=1, H=4, T=512, D=64, fp32, q, k, v ~ N(0,1) from one seed drawn in q, k, v order; the
+    fp32 kernel path (dot_precision="ieee") against the oracle, within 1e-4 relative
+    (||delta||_inf / ||ref||_inf)."""
+    g = torch.Generator().manual_seed(0)
+    q, k, v = (torch.randn(1, 4, 512, 64, generator=g) for _ in range(3))
+    got = kernels.selective_attention_forward(q.to(cuda), k.to(cuda), v.to(cuda), dot_precision="ieee")
+    want = sa_oracle.attention(q.double(), k.double(), v.double())
+    rel = (got.cpu().double() - want).abs().max() / want.abs().max()
+    assert rel.item() < 1e-4, rel.item()
+    # and the fp32 listing in the reference's own form (kernels.selective_attention_reference)
+    lst = kernels.selective_attention_reference(q, k, v)
+    assert ((lst.double() - want).abs().max() / want.abs().max()).item() < 1e-5
+
+
+def test_c5_per_head_slice_bf16_within_2e_2(cuda):
+    """C5 parity on a T=2048 slice: per-head selection (every head its own selector), bf16 operands,
+    k scaled by 2 on a random 10% of key positions; out, dq, dk, dv within 2e-2 max-abs against the
+    per-head oracle (fp32 tensors holding bf16 values, so the gradients stay fp32)."""
+    g = torch.Generator().manual_seed(55)
+    b, h, t, d = 2, 16, 2048, 64
+    q, k, v, do = (torch.randn(b, h, t, d, generator=g) for _ in range(4))
+    boost = torch.rand(b, h, t, 1, generator=g) < 0.1
+    k = torch.where(boost, 2.0 * k, k)
+    q, k, v, do = (x.bfloat16().float() for x in (q, k, v, do))
+    r = lambda x: x.reshape(b * h, 1, t, d)
+    qq, kk, vv = (r(x).to(cuda).requires_grad_(True) for x in (q, k, v))
+    out = kernels.selective_attention(qq, kk, vv, dot_precision="bf16")
+    out.backward(r(do).to(cuda))
+    errs = {}
+    for hh in range(0, b * h, 8):   # the oracle per sequence (each one head), 4 of the 32
+        sl = slice(hh, hh + 1)
+        rq, rk, rv = (x[sl].double().requires_grad_(True) for x in (r(q), r(k), r(v)))
+        ref = sa_oracle.attention(rq, rk, rv)
+        ref.backward(r(do)[sl].double())
+        for name, got, want in (("out", out.detach()[sl], ref.detach()), ("dq", qq.grad[sl], rq.grad),
+                                ("dk", kk.grad[sl], rk.grad), ("dv", vv.grad[sl], rv.grad)):
+            errs[name] = max(errs.get(name, 0.0), (got.cpu().double() - want).abs().max().item())
+    print("C5 slice max-abs errors:", errs, flush=True)
+    assert all(e < 2e-2 for e in errs.values()), errs
