@@ -332,6 +332,25 @@ __device__ __forceinline__ float dpp_shift(float v) {
   return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, ROW_MASK, 0xF, true));
 }
 
+// Exclusive prefix sums over lanes 0..31 and, separately, 32..63, of 16 values at once, step by step
+// across the 16 (each DPP step then has 16 independent instructions and no read-after-write
+// hazard waits between them).
+__device__ __forceinline__ void excl_scan32x16(f32x16& x) {
+  f32x16 s = x;
+#pragma unroll
+  for (int i = 0; i < 16; ++i) s[i] += dpp_shift<0x111, 0xF>(s[i]);   // row_shr:1
+#pragma unroll
+  for (int i = 0; i < 16; ++i) s[i] += dpp_shift<0x112, 0xF>(s[i]);   // row_shr:2
+#pragma unroll
+  for (int i = 0; i < 16; ++i) s[i] += dpp_shift<0x114, 0xF>(s[i]);   // row_shr:4
+#pragma unroll
+  for (int i = 0; i < 16; ++i) s[i] += dpp_shift<0x118, 0xF>(s[i]);   // row_shr:8
+#pragma unroll
+  for (int i = 0; i < 16; ++i) s[i] += dpp_shift<0x142, 0xA>(s[i]);   // row_bcast:15 into rows 1, 3
+#pragma unroll
+  for (int i = 0; i < 16; ++i) x[i] = s[i] - x[i];
+}
+
 // Exclusive prefix sum over lanes 0..31 and, separately, 32..63.
 __device__ __forceinline__ float excl_scan32(float x) {
   float s = x;
@@ -411,7 +430,10 @@ __global__ __launch_bounds__(NTHREADS) void sel_scan_kernel(
 
 // ---------------------------------------------------------------------------------------------
 // Forward. grid (ceil(NBq/4), nseq * H/G); wavefront w of block x owns query block
-// (gridDim.x-1-x)*4 + w (heavy causal rows launch first) of heads [gi*G, gi*G+G).
+// (gridDim.x-1-x)*4 + w (heavy causal rows launch first) of heads [gi*G, gi*G+G). Key tiles are
+// visited newest first, so each row's maximum is usually settled by its diagonal tile and later
+// tiles rarely trigger a rescale of the output (skipped when no lane's maximum rises). The next
+// tile's K, V^T and carry rows are loaded while the current one is computed (double-buffered LDS).
 
 template <class OP, int D, int G>
 __global__ __launch_bounds__(NTHREADS) void fwd_kernel(
@@ -427,9 +449,13 @@ __global__ __launch_bounds__(NTHREADS) void fwd_kernel(
   constexpr int LDK = D + OP::KPAD;
   constexpr int LDV = TILE + OP::TPAD;
   constexpr int AS = OP::acc_steps;
+  constexpr int NH = G + 1;
+  constexpr int TILE_BYTES = (NH * TILE * LDK + G * D * LDV) * (int)sizeof(elem);
+  constexpr int NBUF = 2 * TILE_BYTES <= 120 * 1024 ? 2 : 1;
 
-  __shared__ __attribute__((aligned(16))) elem sK[G + 1][TILE * LDK];
-  __shared__ __attribute__((aligned(16))) elem sVt[G][D * LDV];
+  __shared__ __attribute__((aligned(16))) elem sK[NBUF][NH][TILE * LDK];
+  __shared__ __attribute__((aligned(16))) elem sVt[NBUF][G][D * LDV];
+  __shared__ __attribute__((aligned(16))) float sC[NBUF][NWAVES][TILE];   // carry rows, log2 units
 
   const int tid = threadIdx.x, lane = tid & 63, wave = wave_id();
   const int n = lane & 31, h = lane >> 5;
@@ -483,89 +509,148 @@ __global__ __launch_bounds__(NTHREADS) void fwd_kernel(
     damp = fminf(1.f, train_len / (float)(q_abs + 1));
     if (damp_mode == 2) damp = sqrtf(damp);
   }
-  const float* carry_row = carry + ((int64_t)b * NBq + min(rb, NBq - 1)) * Tk;
 
-  for (int kt = 0; kt < wg_end; ++kt) {
+  // Staging of one key tile: K of the group (+ head 0's), V^T of the group, and the carry rows of
+  // the workgroup's four query blocks (threads 0..127: wavefront w's row, key tid % 32).
+  RowTile<elem, D> nK[NH];
+  ColTile<elem, D> nVt[G];
+  float nC = 0.f;
+  auto load_tile = [&](int kt) {
     const int kbase = kt * TILE;
-    __syncthreads();
 #pragma unroll
     for (int g = 0; g < G; ++g) {
-      stage_rows<elem, D, LDK>(sK[g], k + (seq_row + hd0 + g) * kvs, D, kbase, Tk, tid);
-      stage_cols<elem, D, LDV>(sVt[g], vt + (seq_row + hd0 + g) * D * ldv, ldv, kbase, Tk, tid);
+      nK[g].load(k + (seq_row + hd0 + g) * kvs, D, kbase, Tk, tid);
+      nVt[g].load(vt + (seq_row + hd0 + g) * D * ldv, ldv, kbase, tid);
     }
-    if (!has_h0) stage_rows<elem, D, LDK>(sK[G], k + seq_row * kvs, D, kbase, Tk, tid);
-    __syncthreads();
-    if (kt >= my_end) continue;
-
-    const bool diag = (kbase + TILE - 1 > q_off + rb * TILE) || (kbase + TILE > Tk);
-
-    // head 0 logits (keys x queries) -> selection S -> F (log2 units)
-    f32x16 l0 = zero16();
-    {
-      const elem* k0s = has_h0 ? sK[0] : sK[G];
-#pragma unroll
-      for (int s = 0; s < NS; ++s)
-        l0 = OP::mma(OP::ld_std(k0s, LDK, n, h, s), has_h0 ? qf[0][s] : q0f[s], l0);
-    }
-    f32x16 fs;
-#pragma unroll
-    for (int i = 0; i < 16; ++i) {
-      const int j = kbase + crow(i, h);
-      const float sv = l0[i] * scale;
-      const bool gate = (j >= exempt) && (j < q_abs) && (sv > 0.f);
-      const float sel = gate ? sv : 0.f;
-      const float cj = (j < Tk) ? carry_row[j] : 0.f;
-      fs[i] = (cj + excl_scan32(sel)) * (LOG2E * damp);
-    }
-
+    if (!has_h0) nK[G].load(k + seq_row * kvs, D, kbase, Tk, tid);
+    const int w = (tid >> 5) & (NWAVES - 1);
+    const int rbw = min(qsb * NWAVES + w, NBq - 1);
+    const int jj = kbase + (tid & (TILE - 1));
+    const float c = carry[((int64_t)b * NBq + rbw) * Tk + min(jj, Tk - 1)];
+    nC = (jj < Tk) ? c * LOG2E : 0.f;
+  };
+  auto store_tile = [&](int buf) {
 #pragma unroll
     for (int g = 0; g < G; ++g) {
-      f32x16 lg;
-      if (g == 0 && has_h0) {
-        lg = l0;
-      } else {
-        lg = zero16();
+      nK[g].template store<LDK>(sK[buf][g], tid);
+      nVt[g].template store<LDV>(sVt[buf][g], tid);
+    }
+    if (!has_h0) nK[G].template store<LDK>(sK[buf][G], tid);
+    if (tid < NWAVES * TILE) sC[buf][tid >> 5][tid & (TILE - 1)] = nC;
+  };
+
+  load_tile(wg_end - 1);
+  store_tile(0);
+  __syncthreads();
+
+  for (int t = 0; t < wg_end; ++t) {
+    const int kt = wg_end - 1 - t;
+    const int buf = NBUF == 2 ? (t & 1) : 0;
+    if (t + 1 < wg_end) load_tile(kt - 1);
+    if (kt < my_end) {
+      const int kbase = kt * TILE;
+      auto body = [&](auto edge_tag) {
+        constexpr bool EDGE = decltype(edge_tag)::value;
+        // head 0 logits (keys x queries) -> selection (log2 units) -> F
+        f32x16 l0 = zero16();
+        {
+          const elem* k0s = has_h0 ? sK[buf][0] : sK[buf][G];
 #pragma unroll
-        for (int s = 0; s < NS; ++s) lg = OP::mma(OP::ld_std(sK[g], LDK, n, h, s), qf[g][s], lg);
-      }
-      float zmax = -INFINITY;
-#pragma unroll
-      for (int i = 0; i < 16; ++i) {
-        float z = lg[i] * sl2 - fs[i];
-        if (diag) {
-          const int j = kbase + crow(i, h);
-          if (j > q_abs || j >= Tk) z = -INFINITY;
+          for (int s = 0; s < NS; ++s)
+            l0 = OP::mma(OP::ld_std(k0s, LDK, n, h, s), has_h0 ? qf[0][s] : q0f[s], l0);
         }
-        lg[i] = z;
-        zmax = fmaxf(zmax, z);
-      }
-      zmax = fmaxf(zmax, xor32(zmax));
-      const float m_new = fmaxf(m[g], zmax);
-      const float alpha = fast_exp2(m[g] - m_new);
-      m[g] = m_new;
-      float psum = 0.f;
+        f32x16 fs;
 #pragma unroll
-      for (int i = 0; i < 16; ++i) {
-        const float p = fast_exp2(lg[i] - m_new);
-        lg[i] = p;
-        psum += p;
-      }
-      l[g] = l[g] * alpha + psum;
+        for (int i = 0; i < 16; ++i) {
+          const float sv = l0[i] * sl2;
+          if constexpr (EDGE) {
+            const int j = kbase + crow(i, h);
+            fs[i] = (j >= exempt && j < q_abs && sv > 0.f) ? sv : 0.f;
+          } else {
+            fs[i] = fmaxf(sv, 0.f);
+          }
+        }
+        excl_scan32x16(fs);   // selection by the block's earlier queries
 #pragma unroll
-      for (int db = 0; db < DB; ++db) {
+        for (int a = 0; a < 4; ++a) {
+          const float4 c4 = *reinterpret_cast<const float4*>(&sC[buf][wave][8 * a + 4 * h]);
+          fs[4 * a] += c4.x;
+          fs[4 * a + 1] += c4.y;
+          fs[4 * a + 2] += c4.z;
+          fs[4 * a + 3] += c4.w;
+        }
+        if (damp_mode != 0) {
 #pragma unroll
-        for (int i = 0; i < 16; ++i) o[g][db][i] *= alpha;
+          for (int i = 0; i < 16; ++i) fs[i] *= damp;
+        }
+
 #pragma unroll
-        for (int s = 0; s < AS; ++s)
-          o[g][db] = OP::mma(OP::ld_perm(sVt[g], LDV, db * 32 + n, h, s), OP::from_acc(lg, s), o[g][db]);
-      }
+        for (int g = 0; g < G; ++g) {
+          f32x16 lg;
+          if (g == 0 && has_h0) {
+            lg = l0;
+          } else {
+            lg = zero16();
+#pragma unroll
+            for (int s = 0; s < NS; ++s) lg = OP::mma(OP::ld_std(sK[buf][g], LDK, n, h, s), qf[g][s], lg);
+          }
+          float zmax = -INFINITY;
+#pragma unroll
+          for (int i = 0; i < 16; ++i) {
+            float z = fmaf(lg[i], sl2, -fs[i]);
+            if constexpr (EDGE) {
+              const int j = kbase + crow(i, h);
+              if (j > q_abs || j >= Tk) z = -INFINITY;
+            }
+            lg[i] = z;
+            zmax = fmaxf(zmax, z);
+          }
+          const Halves zh = halves(zmax);
+          const float m_new = fmaxf(m[g], fmaxf(zh.lo, zh.hi));
+          if (__any(m_new > m[g])) {   // some row's maximum rose: rescale what was accumulated
+            const float alpha = (m_new == -INFINITY) ? 1.f : fast_exp2(m[g] - m_new);
+            m[g] = m_new;
+            l[g] *= alpha;
+#pragma unroll
+            for (int db = 0; db < DB; ++db)
+#pragma unroll
+              for (int i = 0; i < 16; ++i) o[g][db][i] *= alpha;
+          }
+          const float mu = (m[g] == -INFINITY) ? 0.f : m[g];   // a row with no key yet
+          float psum = 0.f;
+#pragma unroll
+          for (int i = 0; i < 16; ++i) {
+            const float p = fast_exp2(lg[i] - mu);
+            lg[i] = p;
+            psum += p;
+          }
+          l[g] += psum;
+          frag pf[AS];
+#pragma unroll
+          for (int s = 0; s < AS; ++s) pf[s] = OP::from_acc(lg, s);
+#pragma unroll
+          for (int db = 0; db < DB; ++db)
+#pragma unroll
+            for (int s = 0; s < AS; ++s)
+              o[g][db] = OP::mma(OP::ld_perm(sVt[buf][g], LDV, db * 32 + n, h, s), pf[s], o[g][db]);
+        }
+      };
+      // interior: every key of the tile strictly precedes every query of the block (j < r, so the
+      // selection gate is the logit's sign alone) and lies inside the sequence
+      const bool edge = (kbase + TILE - 1 >= q_off + rb * TILE) || (kbase + TILE > Tk) || kbase < exempt;
+      if (edge) body(std::true_type{});
+      else body(std::false_type{});
     }
+    if constexpr (NBUF == 1) __syncthreads();   // the one buffer is free again
+    if (t + 1 < wg_end) store_tile(NBUF == 2 ? buf ^ 1 : 0);
+    __syncthreads();
   }
 
   if (rb >= NBq || q_rel >= Tq) return;
 #pragma unroll
   for (int g = 0; g < G; ++g) {
-    const float ltot = l[g] + xor32(l[g]);
+    const Halves lh = halves(l[g]);
+    const float ltot = lh.lo + lh.hi;
     const float inv = 1.f / ltot;
     const int64_t row = (seq_row + hd0 + g) * Tq + q_rel;
     float* orow = out + row * D;
@@ -971,7 +1056,7 @@ __global__ __launch_bounds__(NTHREADS, SA_BWD_MIN_BLOCKS) void bwd_kv_kernel(
           acc_t(dk0t, sQt[buf][G], gp, big_tile(gp));
         }
       };
-      const bool edge = (qbase < key0 + TILE - 1) || (qbase + TILE > T) || (key0 + TILE > T) || key0 < exempt;
+      const bool edge = (qbase <= key0 + TILE - 1) || (qbase + TILE > T) || (key0 + TILE > T) || key0 < exempt;
       if (!SPLIT_BODY || edge) body(std::true_type{});   // the masked body is right on every tile
       else body(std::false_type{});
     }
@@ -1239,7 +1324,7 @@ __global__ __launch_bounds__(NTHREADS, SA_BWD_MIN_BLOCKS) void bwd_dq_kernel(
           acc_xk(dq0acc, gp, sKt[buf][G], big_tile(gp));
         }
       };
-      const bool edge = (kbase + TILE - 1 > qbase) || (qbase + TILE > T) || (kbase + TILE > T) || kbase < exempt;
+      const bool edge = (kbase + TILE - 1 >= qbase) || (qbase + TILE > T) || (kbase + TILE > T) || kbase < exempt;
       if (!SPLIT_BODY || edge) body(std::true_type{});   // the masked body is right on every tile
       else body(std::false_type{});
     }
@@ -1348,12 +1433,15 @@ inline int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
 
 inline int launch_status() { return hipGetLastError() == hipSuccess ? SA_OK : SA_ERR_LAUNCH; }
 
+#ifndef SA_FWD_GROUP_D64
+#define SA_FWD_GROUP_D64 1
+#endif
 int auto_group(int dtype, int64_t D, int64_t heads, int requested, bool backward) {
   int g = requested;
   if (g <= 0) {
     if (dtype == SA_DTYPE_F32) g = 1;
     else if (backward) g = (D <= 32) ? 2 : 1;
-    else g = (D <= 32) ? 4 : (D <= 64 ? 2 : 1);
+    else g = (D <= 32) ? 4 : (D <= 64 ? SA_FWD_GROUP_D64 : 1);
   }
   int cap = (dtype == SA_DTYPE_F32) ? 1 : (backward ? 2 : 4);
   if (D >= 128 || (backward && D >= 64)) cap = 1;

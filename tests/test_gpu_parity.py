@@ -390,3 +390,20 @@ def test_c5_per_head_slice_bf16_within_2e_2(cuda):
             errs[name] = max(errs.get(name, 0.0), (got.cpu().double() - want).abs().max().item())
     print("C5 slice max-abs errors:", errs, flush=True)
     assert all(e < 2e-2 for e in errs.values()), errs
+
+
+@pytest.mark.parametrize("chunk", [7, 13, 33])
+@pytest.mark.parametrize("exempt", [1, 16])
+def test_chunked_prefill_unaligned_offsets(cuda, chunk, exempt):
+    """Chunk offsets that are not multiples of the 32-query tile: the key tile ending at a chunk's
+    first query must still exclude that query's own key from its selection."""
+    print(f"case prefill unaligned chunk={chunk} exempt={exempt}", flush=True)
+    q, k, v = _qkv(2, 4, 160, 32, seed=chunk + exempt, scale=1.5)
+    qd, kd, vd = (t.to(cuda) for t in (q, k, v))
+    state = torch.zeros(2, 160, device=cuda)
+    outs = [kernels.selective_attention_prefill(qd[:, :, c0:c0 + chunk], kd[:, :, :c0 + chunk], vd[:, :, :c0 + chunk],
+                                                state, c0, dot_precision="ieee", exempt=exempt)
+            for c0 in range(0, 160, chunk)]
+    want = sa_oracle.attention(q.double(), k.double(), v.double(), exempt)
+    _close(torch.cat(outs, dim=2).cpu(), want, 2e-5, 2e-5, "chunked out")
+    _close(state.cpu(), sa_oracle.selection_totals(q.double(), k.double(), exempt), 2e-4, 2e-5, "state")
