@@ -716,22 +716,36 @@ __global__ __launch_bounds__(NTHREADS) void fill_zero_kernel(float4* __restrict_
 }
 
 // ---------------------------------------------------------------------------------------------
-// Backward kernel shape. SA_BWD_PIPE 1: the next tile's global loads are issued before the current
-// tile is computed (double-buffered LDS when it fits); 0: load, store, compute in turn, leaving the
-// overlap to a second workgroup on the CU. SA_BWD_MIN_BLOCKS: workgroups per CU the register
+// Backward kernel shapes. *_PIPE 1: the next tile's global loads are issued before the current tile
+// is computed (double-buffered LDS when it fits); 0: load, store, compute in turn, leaving the
+// overlap to another workgroup on the CU. *_MIN_BLOCKS: workgroups per CU the register
 // allocation must allow.
-#ifndef SA_BWD_PIPE
-#define SA_BWD_PIPE 1
+// The key side holds K, V and the dK, dV sums in registers and runs best at one workgroup per CU
+// with its loads pipelined; the query side fits two workgroups per CU without the staging
+// registers, and the second workgroup hides its LDS and memory latency better than pipelining.
+#ifndef SA_KV_PIPE
+#define SA_KV_PIPE 0
 #endif
-#ifndef SA_BWD_MIN_BLOCKS
-#define SA_BWD_MIN_BLOCKS 1
+#ifndef SA_KV_MIN_BLOCKS
+#define SA_KV_MIN_BLOCKS 1
 #endif
-constexpr bool BWD_PIPE = SA_BWD_PIPE != 0;
+#ifndef SA_DQ_PIPE
+#define SA_DQ_PIPE 0
+#endif
+#ifndef SA_DQ_MIN_BLOCKS
+#define SA_DQ_MIN_BLOCKS 2
+#endif
+// two query-side workgroups per CU where their registers allow it (bf16, head dim <= 64)
+template <class OP, int D>
+constexpr int dq_min_blocks() { return (sizeof(typename OP::elem) == 2 && D <= 64) ? SA_DQ_MIN_BLOCKS : 1; }
 // A second, mask-free copy of the tile body for interior tiles; kept to bf16 head dims <= 64,
 // where the registers allow it (the head-dim-128 backward with both copies is also beyond what
 // this compiler's AGPR rewrite pass handles).
+#ifndef SA_SPLIT_BODY
+#define SA_SPLIT_BODY 0
+#endif
 template <class OP, int D>
-constexpr bool split_body() { return sizeof(typename OP::elem) == 2 && D <= 64; }
+constexpr bool split_body() { return SA_SPLIT_BODY && sizeof(typename OP::elem) == 2 && D <= 64; }
 
 // ---------------------------------------------------------------------------------------------
 // Backward helpers on (queries x keys) C-layout tiles: lane n holds key j = key0 + n, rows are the
@@ -739,12 +753,14 @@ constexpr bool split_body() { return sizeof(typename OP::elem) == 2 && D <= 64; 
 
 // Head 0's selection on a tile of its raw logits l0, in log2 units: sel = relu(s log2e l0) where
 // exempt <= j < r < T, and the history F[r, j] = hist2 + sum of sel over the tile's earlier rows
-// (the running sum runs down the rows; the half-wavefronts exchange partial sums). The gate of
-// the gradient path is sel > 0. EDGE (wave-uniform) marks tiles where some pair fails
+// (the running sum runs down the rows; the half-wavefronts exchange partial sums). Bit i of `gate`
+// is sel[i] > 0, the gate of the gradient path. EDGE (wave-uniform) marks tiles where some pair fails
 // exempt <= j < r < T; elsewhere the gate is the sign of the logit alone.
 template <bool EDGE>
 __device__ __forceinline__ void selection_tile(const f32x16& l0, float hist2, int qbase, int j, int T, int exempt,
-                                               float sl2, int h, f32x16& fs, f32x16& sel) {
+                                               float sl2, int h, f32x16& fs, uint32_t& gate) {
+  f32x16 sel;
+  gate = 0;
 #pragma unroll
   for (int i = 0; i < 16; ++i) {
     const float sv = l0[i] * sl2;
@@ -755,6 +771,7 @@ __device__ __forceinline__ void selection_tile(const f32x16& l0, float hist2, in
     } else {
       sel[i] = fmaxf(sv, 0.f);
     }
+    gate |= sel[i] > 0.f ? (1u << i) : 0u;
   }
   float run = hist2;
 #pragma unroll
@@ -771,8 +788,8 @@ __device__ __forceinline__ void selection_tile(const f32x16& l0, float hist2, in
 }
 
 // Selection gradient path: U[r, j] = u_in + sum of z over the tile's later rows, and
-// g = -[sel > 0] U. Returns u_in + the sum over the whole tile (U entering the tile above).
-__device__ __forceinline__ float gpath_tile(const f32x16& z, float u_in, const f32x16& sel, int h, f32x16& gp) {
+// g = -gate U (gate bit i: sel[i] > 0). Returns u_in + the sum over the whole tile (U entering the tile above).
+__device__ __forceinline__ float gpath_tile(const f32x16& z, float u_in, uint32_t gate, int h, f32x16& gp) {
   float run = u_in;
 #pragma unroll
   for (int a = 3; a >= 0; --a) {
@@ -781,7 +798,7 @@ __device__ __forceinline__ float gpath_tile(const f32x16& z, float u_in, const f
 #pragma unroll
     for (int t = 3; t >= 0; --t) {
       const int i = 4 * a + t;
-      gp[i] = sel[i] > 0.f ? -p : 0.f;
+      gp[i] = ((gate >> i) & 1u) ? -p : 0.f;
       p += z[i];
     }
     run = (run + g.hi) + g.lo;
@@ -833,7 +850,7 @@ __device__ __forceinline__ bool big_tile(const f32x16& x) {
 // group: the group holding head 0 folds it into head 0's dz; the others add their share to dk0x.
 
 template <class OP, int D, int G>
-__global__ __launch_bounds__(NTHREADS, SA_BWD_MIN_BLOCKS) void bwd_kv_kernel(
+__global__ __launch_bounds__(NTHREADS, SA_KV_MIN_BLOCKS) void bwd_kv_kernel(
     const typename OP::elem* __restrict__ q, const typename OP::elem* __restrict__ k,
     const typename OP::elem* __restrict__ v, const typename OP::elem* __restrict__ qt,
     const typename OP::elem* __restrict__ dout, const typename OP::elem* __restrict__ dot,
@@ -848,10 +865,11 @@ __global__ __launch_bounds__(NTHREADS, SA_BWD_MIN_BLOCKS) void bwd_kv_kernel(
   constexpr int LDV = TILE + OP::TPAD;
   constexpr int AS = OP::acc_steps;
   constexpr int NH = G + 1;   // staged heads: the group, then head 0 when outside the group
+  constexpr bool KV_PIPE = SA_KV_PIPE != 0;
   constexpr bool SPLIT_BODY = split_body<OP, D>();
   // two buffers (the tile being computed, the next one being written) when they fit in LDS
   constexpr int TILE_BYTES = (NH * (TILE * LDK + D * LDV) + G * (TILE * LDK + D * LDV)) * (int)sizeof(elem);
-  constexpr int NBUF = (BWD_PIPE && 2 * TILE_BYTES <= 120 * 1024) ? 2 : 1;
+  constexpr int NBUF = (KV_PIPE && 2 * TILE_BYTES <= 120 * 1024) ? 2 : 1;
 
   __shared__ __attribute__((aligned(16))) elem sQ[NBUF][NH][TILE * LDK];
   __shared__ __attribute__((aligned(16))) elem sQt[NBUF][NH][D * LDV];
@@ -977,7 +995,7 @@ __global__ __launch_bounds__(NTHREADS, SA_BWD_MIN_BLOCKS) void bwd_kv_kernel(
   const bool split_keys = key0 < exempt;
 
   float hist_next = 0.f;
-  if constexpr (BWD_PIPE) {
+  if constexpr (KV_PIPE) {
     load_tile(NB - 1);
     hist_next = carry_col[(int64_t)(NB - 1) * T];
     store_tile(0);
@@ -989,7 +1007,7 @@ __global__ __launch_bounds__(NTHREADS, SA_BWD_MIN_BLOCKS) void bwd_kv_kernel(
     const int qbase = qb * TILE;
     const int buf = NBUF == 2 ? (t & 1) : 0;
     float hist;
-    if constexpr (BWD_PIPE) {
+    if constexpr (KV_PIPE) {
       hist = hist_next;
       if (t + 1 < ntiles) {
         load_tile(qb - 1);
@@ -1011,8 +1029,9 @@ __global__ __launch_bounds__(NTHREADS, SA_BWD_MIN_BLOCKS) void bwd_kv_kernel(
         f32x16 l0 = zero16();
 #pragma unroll
         for (int s = 0; s < NS; ++s) l0 = OP::mma(OP::ld_std(q0s, LDK, n, h, s), has_h0 ? kf[0][s] : k0f[s], l0);
-        f32x16 fs, sel;
-        selection_tile<EDGE>(l0, (j < T) ? hist * LOG2E : 0.f, qbase, j, T, exempt, sl2, h, fs, sel);
+        f32x16 fs;
+        uint32_t gate;
+        selection_tile<EDGE>(l0, (j < T) ? hist * LOG2E : 0.f, qbase, j, T, exempt, sl2, h, fs, gate);
 
         f32x16 dzsum, dz0;
 #pragma unroll
@@ -1046,7 +1065,7 @@ __global__ __launch_bounds__(NTHREADS, SA_BWD_MIN_BLOCKS) void bwd_kv_kernel(
         }
 
         f32x16 gp;
-        ucarry = gpath_tile(dzsum, ucarry, sel, h, gp);
+        ucarry = gpath_tile(dzsum, ucarry, gate, h, gp);
         if (has_h0) {
           f32x16 dzh;
 #pragma unroll
@@ -1060,7 +1079,7 @@ __global__ __launch_bounds__(NTHREADS, SA_BWD_MIN_BLOCKS) void bwd_kv_kernel(
       if (!SPLIT_BODY || edge) body(std::true_type{});   // the masked body is right on every tile
       else body(std::false_type{});
     }
-    if constexpr (BWD_PIPE) {
+    if constexpr (KV_PIPE) {
       if constexpr (NBUF == 1) __syncthreads();   // the one buffer is free again
       if (t + 1 < ntiles) store_tile(NBUF == 2 ? buf ^ 1 : 0);
       __syncthreads();
@@ -1103,7 +1122,7 @@ __global__ __launch_bounds__(NTHREADS, SA_BWD_MIN_BLOCKS) void bwd_kv_kernel(
 // and K^T from LDS (as the B operand).
 
 template <class OP, int D, int G>
-__global__ __launch_bounds__(NTHREADS, SA_BWD_MIN_BLOCKS) void bwd_dq_kernel(
+__global__ __launch_bounds__(NTHREADS, (dq_min_blocks<OP, D>())) void bwd_dq_kernel(
     const typename OP::elem* __restrict__ q, const typename OP::elem* __restrict__ k,
     const typename OP::elem* __restrict__ v, const typename OP::elem* __restrict__ kt,
     const typename OP::elem* __restrict__ dout, const float* __restrict__ lse, const float* __restrict__ dbar,
@@ -1118,9 +1137,10 @@ __global__ __launch_bounds__(NTHREADS, SA_BWD_MIN_BLOCKS) void bwd_dq_kernel(
   constexpr int LDZ = TILE + OP::KPAD;
   constexpr int AS = OP::acc_steps;
   constexpr int NH = G + 1;
+  constexpr bool DQ_PIPE = SA_DQ_PIPE != 0;
   constexpr bool SPLIT_BODY = split_body<OP, D>();
   constexpr int TILE_BYTES = (NH * (TILE * LDK + D * LDKT) + G * TILE * LDK) * (int)sizeof(elem);
-  constexpr int NBUF = (BWD_PIPE && 2 * TILE_BYTES <= 120 * 1024) ? 2 : 1;
+  constexpr int NBUF = (DQ_PIPE && 2 * TILE_BYTES <= 120 * 1024) ? 2 : 1;
 
   __shared__ __attribute__((aligned(16))) elem sK[NBUF][NH][TILE * LDK];
   __shared__ __attribute__((aligned(16))) elem sKt[NBUF][NH][D * LDKT];
@@ -1128,6 +1148,13 @@ __global__ __launch_bounds__(NTHREADS, SA_BWD_MIN_BLOCKS) void bwd_dq_kernel(
   __shared__ __attribute__((aligned(16))) elem sZ[NWAVES][TILE * LDZ];
   __shared__ __attribute__((aligned(16))) float sLse[NWAVES][G][TILE];
   __shared__ __attribute__((aligned(16))) float sDb[NWAVES][G][TILE];
+  // Each wavefront's own Q and dO rows (A operands) are read from LDS per tile instead of being held
+  // in registers, when they fit beside the key tiles in half the CU's LDS: the registers they free
+  // let two workgroups share a CU.
+  constexpr int OTHER_LDS = NBUF * TILE_BYTES + NWAVES * (TILE * LDZ * (int)sizeof(elem) + 2 * G * TILE * 4);
+  constexpr bool QLDS = OTHER_LDS + 2 * NWAVES * G * TILE * LDK * (int)sizeof(elem) <= 80 * 1024;
+  __shared__ __attribute__((aligned(16))) elem sQw[QLDS ? NWAVES : 1][G][QLDS ? TILE * LDK : 8];
+  __shared__ __attribute__((aligned(16))) elem sdOw[QLDS ? NWAVES : 1][G][QLDS ? TILE * LDK : 8];
 
   const int tid = threadIdx.x, lane = tid & 63, wave = wave_id();
   const int n = lane & 31, h = lane >> 5;
@@ -1148,16 +1175,49 @@ __global__ __launch_bounds__(NTHREADS, SA_BWD_MIN_BLOCKS) void bwd_dq_kernel(
   const float* carry_row = carry + ((int64_t)b * NB + qb_c) * T;
   const float* urow = ucheck + (((int64_t)gi * nseq + b) * NB + qb_c) * T;
 
-  // Query-side operands in registers (A operands: lane = query row).
-  frag qa[G][NS], doa[G][NS], q0a[NS];
+  // Query-side operands (A operands: lane = query row): the group's Q and dO rows in this
+  // wavefront's LDS, head 0's Q rows in registers.
+  frag q0a[NS];
+  frag qa[QLDS ? 1 : G][NS], doa[QLDS ? 1 : G][NS];
+  if constexpr (!QLDS) {
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+      const int64_t row = seq_row + hd0 + g;
+#pragma unroll
+      for (int s = 0; s < NS; ++s) {
+        qa[g][s] = ld_std_bounded<OP>(q + row * T * D, D, qbase + n, T, h, s);
+        doa[g][s] = ld_std_bounded<OP>(dout + row * T * D, D, qbase + n, T, h, s);
+      }
+    }
+  } else {
+    constexpr int EPC = 16 / (int)sizeof(elem), CPR = D / EPC;
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+      const int64_t row = seq_row + hd0 + g;
+      for (int c = lane; c < TILE * CPR; c += 64) {
+        const int r = c / CPR, cc = (c % CPR) * EPC;
+        const int rr = min(qbase + r, T - 1);
+        const bool ok = qbase + r < T;
+        const uint4 xq = *reinterpret_cast<const uint4*>(q + (row * T + rr) * D + cc);
+        const uint4 xo = *reinterpret_cast<const uint4*>(dout + (row * T + rr) * D + cc);
+        *reinterpret_cast<uint4*>(&sQw[wave][g][r * LDK + cc]) =
+            ok ? xq : make_uint4(0u, 0u, 0u, 0u);
+        *reinterpret_cast<uint4*>(&sdOw[wave][g][r * LDK + cc]) =
+            ok ? xo : make_uint4(0u, 0u, 0u, 0u);
+      }
+    }
+  }
+  auto q_frag = [&](int g, int s) -> frag {
+    if constexpr (QLDS) return OP::ld_std(sQw[wave][g], LDK, n, h, s);
+    else return qa[g][s];
+  };
+  auto do_frag = [&](int g, int s) -> frag {
+    if constexpr (QLDS) return OP::ld_std(sdOw[wave][g], LDK, n, h, s);
+    else return doa[g][s];
+  };
 #pragma unroll
   for (int g = 0; g < G; ++g) {
     const int64_t row = seq_row + hd0 + g;
-#pragma unroll
-    for (int s = 0; s < NS; ++s) {
-      qa[g][s] = ld_std_bounded<OP>(q + row * T * D, D, qbase + n, T, h, s);
-      doa[g][s] = ld_std_bounded<OP>(dout + row * T * D, D, qbase + n, T, h, s);
-    }
     if (lane < TILE) {
       const int r = qbase + lane;
       sLse[wave][g][lane] = (r < T) ? lse[row * T + r] : 0.f;
@@ -1247,7 +1307,7 @@ __global__ __launch_bounds__(NTHREADS, SA_BWD_MIN_BLOCKS) void bwd_dq_kernel(
   };
 
   float hist_next = 0.f, u_next = 0.f;
-  if constexpr (BWD_PIPE) {
+  if constexpr (DQ_PIPE) {
     load_tile(0);
     key_vals(0, hist_next, u_next);
     store_tile(0);
@@ -1258,7 +1318,7 @@ __global__ __launch_bounds__(NTHREADS, SA_BWD_MIN_BLOCKS) void bwd_dq_kernel(
     const int kbase = ktile * TILE;
     const int buf = NBUF == 2 ? (ktile & 1) : 0;
     float hist, uin;
-    if constexpr (BWD_PIPE) {
+    if constexpr (DQ_PIPE) {
       hist = hist_next;
       uin = u_next;
       if (ktile + 1 < wg_end) {
@@ -1279,9 +1339,11 @@ __global__ __launch_bounds__(NTHREADS, SA_BWD_MIN_BLOCKS) void bwd_dq_kernel(
         const elem* k0s = has_h0 ? sK[buf][0] : sK[buf][G];
         f32x16 l0 = zero16();
 #pragma unroll
-        for (int s = 0; s < NS; ++s) l0 = OP::mma(has_h0 ? qa[0][s] : q0a[s], OP::ld_std(k0s, LDK, n, h, s), l0);
-        f32x16 fs, sel;
-        selection_tile<EDGE>(l0, hist * LOG2E, qbase, j, T, exempt, sl2, h, fs, sel);
+        for (int s = 0; s < NS; ++s)
+          l0 = OP::mma(has_h0 ? q_frag(0, s) : q0a[s], OP::ld_std(k0s, LDK, n, h, s), l0);
+        f32x16 fs;
+        uint32_t gate;
+        selection_tile<EDGE>(l0, hist * LOG2E, qbase, j, T, exempt, sl2, h, fs, gate);
 
         f32x16 zsum, dz0;
 #pragma unroll
@@ -1293,11 +1355,13 @@ __global__ __launch_bounds__(NTHREADS, SA_BWD_MIN_BLOCKS) void bwd_dq_kernel(
           } else {
             lg = zero16();
 #pragma unroll
-            for (int s = 0; s < NS; ++s) lg = OP::mma(qa[g][s], OP::ld_std(sK[buf][g], LDK, n, h, s), lg);
+            for (int s = 0; s < NS; ++s)
+              lg = OP::mma(q_frag(g, s), OP::ld_std(sK[buf][g], LDK, n, h, s), lg);
           }
           f32x16 dp = zero16();
 #pragma unroll
-          for (int s = 0; s < NS; ++s) dp = OP::mma(doa[g][s], OP::ld_std(sV[buf][g], LDK, n, h, s), dp);
+          for (int s = 0; s < NS; ++s)
+            dp = OP::mma(do_frag(g, s), OP::ld_std(sV[buf][g], LDK, n, h, s), dp);
           f32x16 pr, dz;
           p_dz_tile<EDGE>(lg, dp, fs, sLse[wave][g], sDb[wave][g], sl2, qbase, j, T, h, pr, dz);
           if (gg == 0) {
@@ -1314,7 +1378,7 @@ __global__ __launch_bounds__(NTHREADS, SA_BWD_MIN_BLOCKS) void bwd_dq_kernel(
         }
 
         f32x16 gp;
-        gpath_tile(zsum, uin, sel, h, gp);
+        gpath_tile(zsum, uin, gate, h, gp);
         if (has_h0) {
           f32x16 dzh;
 #pragma unroll
@@ -1328,7 +1392,7 @@ __global__ __launch_bounds__(NTHREADS, SA_BWD_MIN_BLOCKS) void bwd_dq_kernel(
       if (!SPLIT_BODY || edge) body(std::true_type{});   // the masked body is right on every tile
       else body(std::false_type{});
     }
-    if constexpr (BWD_PIPE) {
+    if constexpr (DQ_PIPE) {
       if constexpr (NBUF == 1) __syncthreads();   // the one buffer is free again
       if (ktile + 1 < wg_end) store_tile(NBUF == 2 ? buf ^ 1 : 0);
       __syncthreads();
