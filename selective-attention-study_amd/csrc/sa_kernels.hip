@@ -248,6 +248,12 @@ __device__ __forceinline__ void stage_cols(E* s, const E* g, int64_t gld, int co
   }
 }
 
+// Unpadded LDS rows of 64 bf16 (eight 16-byte chunks), chunk c of row r stored at chunk position
+// (c + r + r/8) mod 8. A lane-per-row fragment read (every lane the same logical chunk) then puts
+// any 8 aligned consecutive rows on 8 distinct 16-byte bank groups and any 16 on 16 distinct
+// (32 or 64 four-byte banks), as a padded row stride would, without the padding's bytes.
+__device__ __forceinline__ int swz64(int r, int c) { return r * 64 + (((c + r + (r >> 3)) & 7) << 3); }
+
 // Register-staged tiles for software pipelining: load() issues a tile's global loads into registers
 // (each thread owns PER 16-byte chunks), store() later writes them to LDS, so the loads of the next
 // tile are in flight while the current one is computed.
@@ -720,14 +726,14 @@ __global__ __launch_bounds__(NTHREADS) void fill_zero_kernel(float4* __restrict_
 // is computed (double-buffered LDS when it fits); 0: load, store, compute in turn, leaving the
 // overlap to another workgroup on the CU. *_MIN_BLOCKS: workgroups per CU the register
 // allocation must allow.
-// The key side holds K, V and the dK, dV sums in registers and runs best at one workgroup per CU
-// with its loads pipelined; the query side fits two workgroups per CU without the staging
-// registers, and the second workgroup hides its LDS and memory latency better than pipelining.
+// Both sides fit two workgroups per CU at bf16 head dims <= 64 once their per-wavefront operands
+// (the key side's K and V rows, the query side's Q and dO rows) sit in LDS instead of registers;
+// the second workgroup then hides LDS and memory latency better than pipelining the loads.
 #ifndef SA_KV_PIPE
 #define SA_KV_PIPE 0
 #endif
 #ifndef SA_KV_MIN_BLOCKS
-#define SA_KV_MIN_BLOCKS 1
+#define SA_KV_MIN_BLOCKS 2
 #endif
 #ifndef SA_DQ_PIPE
 #define SA_DQ_PIPE 0
@@ -735,9 +741,11 @@ __global__ __launch_bounds__(NTHREADS) void fill_zero_kernel(float4* __restrict_
 #ifndef SA_DQ_MIN_BLOCKS
 #define SA_DQ_MIN_BLOCKS 2
 #endif
-// two query-side workgroups per CU where their registers allow it (bf16, head dim <= 64)
+// two workgroups per CU where their registers allow it (bf16, head dim <= 64)
 template <class OP, int D>
 constexpr int dq_min_blocks() { return (sizeof(typename OP::elem) == 2 && D <= 64) ? SA_DQ_MIN_BLOCKS : 1; }
+template <class OP, int D, int G>
+constexpr int kv_min_blocks() { return (sizeof(typename OP::elem) == 2 && D <= 64 && G == 1) ? SA_KV_MIN_BLOCKS : 1; }
 // A second, mask-free copy of the tile body for interior tiles; kept to bf16 head dims <= 64,
 // where the registers allow it (the head-dim-128 backward with both copies is also beyond what
 // this compiler's AGPR rewrite pass handles).
@@ -850,7 +858,7 @@ __device__ __forceinline__ bool big_tile(const f32x16& x) {
 // group: the group holding head 0 folds it into head 0's dz; the others add their share to dk0x.
 
 template <class OP, int D, int G>
-__global__ __launch_bounds__(NTHREADS, SA_KV_MIN_BLOCKS) void bwd_kv_kernel(
+__global__ __launch_bounds__(NTHREADS, (kv_min_blocks<OP, D, G>())) void bwd_kv_kernel(
     const typename OP::elem* __restrict__ q, const typename OP::elem* __restrict__ k,
     const typename OP::elem* __restrict__ v, const typename OP::elem* __restrict__ qt,
     const typename OP::elem* __restrict__ dout, const typename OP::elem* __restrict__ dot,
@@ -877,6 +885,13 @@ __global__ __launch_bounds__(NTHREADS, SA_KV_MIN_BLOCKS) void bwd_kv_kernel(
   __shared__ __attribute__((aligned(16))) elem sdOt[NBUF][G][D * LDV];
   __shared__ __attribute__((aligned(16))) float sLse[NBUF][G][TILE];
   __shared__ __attribute__((aligned(16))) float sDb[NBUF][G][TILE];
+  // Each wavefront's K and V rows (and head 0's K rows) are read from LDS per tile instead of being
+  // held in registers, when they fit unpadded (swz64) beside the query tiles in half the CU's LDS:
+  // the registers they free let two workgroups share a CU.
+  constexpr int NKV = 2 * G + 1;   // K, V of each head of the group, then head 0's K
+  constexpr int OTHER_LDS = NBUF * (TILE_BYTES + 2 * G * TILE * 4);
+  constexpr bool KVLDS = sizeof(elem) == 2 && D == 64 && OTHER_LDS + NWAVES * NKV * TILE * D * 2 <= 80 * 1024;
+  __shared__ __attribute__((aligned(16))) elem sKV[KVLDS ? NWAVES : 1][KVLDS ? NKV : 1][KVLDS ? TILE * D : 8];
 
   const int tid = threadIdx.x, lane = tid & 63, wave = wave_id();
   const int n = lane & 31, h = lane >> 5;
@@ -891,23 +906,62 @@ __global__ __launch_bounds__(NTHREADS, SA_KV_MIN_BLOCKS) void bwd_kv_kernel(
   float* uplane = ucheck + ((int64_t)gi * nseq + b) * NB * (int64_t)T;
   const float* carry_col = carry + (int64_t)b * NB * T + (j < T ? j : 0);
 
-  // Key-side operands in registers (B operands: lane = key column).
-  frag kf[G][NS], vf[G][NS], k0f[NS];
+  // Key-side operands (B operands: lane = key column): this wavefront's K and V rows of the group
+  // and head 0's K rows, in its LDS rows or in registers.
+  frag kf[KVLDS ? 1 : G][NS], vf[KVLDS ? 1 : G][NS], k0f[NS];
+  if constexpr (KVLDS) {
+    constexpr int CPR = D / 8;
+    for (int c = lane; c < TILE * CPR; c += 64) {
+      const int r = c / CPR, cc = c % CPR;
+      const int64_t jr = min(key0 + r, T - 1);
+      const bool ok = key0 + r < T;
+      auto put = [&](int x, const elem* src) {
+        const uint4 v4 = *reinterpret_cast<const uint4*>(src + jr * D + cc * 8);
+        *reinterpret_cast<uint4*>(&sKV[wave][x][swz64(r, cc)]) =
+            make_uint4(ok ? v4.x : 0u, ok ? v4.y : 0u, ok ? v4.z : 0u, ok ? v4.w : 0u);
+      };
 #pragma unroll
-  for (int g = 0; g < G; ++g) {
-    const elem* kh = k + (seq_row + hd0 + g) * T * D;
-    const elem* vh = v + (seq_row + hd0 + g) * T * D;
+      for (int g = 0; g < G; ++g) {
+        put(2 * g, k + (seq_row + hd0 + g) * T * D);
+        put(2 * g + 1, v + (seq_row + hd0 + g) * T * D);
+      }
+      if (!has_h0) put(2 * G, k + seq_row * T * D);
+    }
+  } else {
 #pragma unroll
-    for (int s = 0; s < NS; ++s) {
-      kf[g][s] = ld_std_bounded<OP>(kh, D, j, T, h, s);
-      vf[g][s] = ld_std_bounded<OP>(vh, D, j, T, h, s);
+    for (int g = 0; g < G; ++g) {
+      const elem* kh = k + (seq_row + hd0 + g) * T * D;
+      const elem* vh = v + (seq_row + hd0 + g) * T * D;
+#pragma unroll
+      for (int s = 0; s < NS; ++s) {
+        kf[g][s] = ld_std_bounded<OP>(kh, D, j, T, h, s);
+        vf[g][s] = ld_std_bounded<OP>(vh, D, j, T, h, s);
+      }
+    }
+    if (!has_h0) {
+      const elem* kh = k + seq_row * T * D;
+#pragma unroll
+      for (int s = 0; s < NS; ++s) k0f[s] = ld_std_bounded<OP>(kh, D, j, T, h, s);
     }
   }
-  if (!has_h0) {
-    const elem* kh = k + seq_row * T * D;
-#pragma unroll
-    for (int s = 0; s < NS; ++s) k0f[s] = ld_std_bounded<OP>(kh, D, j, T, h, s);
-  }
+  // fragment s of row n (this lane's key) of LDS row block x
+  auto kv_lds = [&](int x, int s) -> frag {
+    if constexpr (KVLDS) return *reinterpret_cast<const frag*>(&sKV[wave][x][swz64(n, 2 * s + h)]);
+    else return OP::zero();
+  };
+  auto k_frag = [&](int g, int s) -> frag {
+    if constexpr (KVLDS) return kv_lds(2 * g, s);
+    else return kf[g][s];
+  };
+  auto v_frag = [&](int g, int s) -> frag {
+    if constexpr (KVLDS) return kv_lds(2 * g + 1, s);
+    else return vf[g][s];
+  };
+  // head 0's K: the group's own when it holds head 0
+  auto k0_frag = [&](int s) -> frag {
+    if constexpr (KVLDS) return kv_lds(has_h0 ? 0 : 2 * G, s);
+    else return has_h0 ? kf[0][s] : k0f[s];
+  };
 
   f32x16 dkt[G][DB], dvt[G][DB], dk0t[DB];
 #pragma unroll
@@ -1028,30 +1082,29 @@ __global__ __launch_bounds__(NTHREADS, SA_KV_MIN_BLOCKS) void bwd_kv_kernel(
         const elem* q0s = has_h0 ? sQ[buf][0] : sQ[buf][G];
         f32x16 l0 = zero16();
 #pragma unroll
-        for (int s = 0; s < NS; ++s) l0 = OP::mma(OP::ld_std(q0s, LDK, n, h, s), has_h0 ? kf[0][s] : k0f[s], l0);
+        for (int s = 0; s < NS; ++s) l0 = OP::mma(OP::ld_std(q0s, LDK, n, h, s), k0_frag(s), l0);
         f32x16 fs;
         uint32_t gate;
         selection_tile<EDGE>(l0, (j < T) ? hist * LOG2E : 0.f, qbase, j, T, exempt, sl2, h, fs, gate);
 
         f32x16 dzsum, dz0;
 #pragma unroll
-        for (int gg = 0; gg < G; ++gg) {
-          const int g = has_h0 ? (gg + 1) % G : gg;   // head 0 last: its dK waits for g
+        for (int g = 0; g < G; ++g) {
           f32x16 lg;
-          if (has_h0 && g == 0) {
+          if (has_h0 && g == 0) {   // head 0 itself: its logits are l0, its dK waits for g
             lg = l0;
           } else {
             lg = zero16();
 #pragma unroll
-            for (int s = 0; s < NS; ++s) lg = OP::mma(OP::ld_std(sQ[buf][g], LDK, n, h, s), kf[g][s], lg);
+            for (int s = 0; s < NS; ++s) lg = OP::mma(OP::ld_std(sQ[buf][g], LDK, n, h, s), k_frag(g, s), lg);
           }
           f32x16 dp = zero16();
 #pragma unroll
-          for (int s = 0; s < NS; ++s) dp = OP::mma(OP::ld_std(sdO[buf][g], LDK, n, h, s), vf[g][s], dp);
+          for (int s = 0; s < NS; ++s) dp = OP::mma(OP::ld_std(sdO[buf][g], LDK, n, h, s), v_frag(g, s), dp);
           f32x16 pr, dz;
           p_dz_tile<EDGE>(lg, dp, fs, sLse[buf][g], sDb[buf][g], sl2, qbase, j, T, h, pr, dz);
           acc_t(dvt[g], sdOt[buf][g], pr, split_keys);   // dV^T += dO^T P
-          if (gg == 0) {
+          if (g == 0) {
             dzsum = dz;
           } else {
 #pragma unroll
