@@ -735,6 +735,7 @@ __global__ __launch_bounds__(NTHREADS) void fill_zero_kernel(float4* __restrict_
 #ifndef SA_KV_MIN_BLOCKS
 #define SA_KV_MIN_BLOCKS 2
 #endif
+
 #ifndef SA_DQ_PIPE
 #define SA_DQ_PIPE 0
 #endif
@@ -746,41 +747,45 @@ template <class OP, int D>
 constexpr int dq_min_blocks() { return (sizeof(typename OP::elem) == 2 && D <= 64) ? SA_DQ_MIN_BLOCKS : 1; }
 template <class OP, int D, int G>
 constexpr int kv_min_blocks() { return (sizeof(typename OP::elem) == 2 && D <= 64 && G == 1) ? SA_KV_MIN_BLOCKS : 1; }
-// A second, mask-free copy of the tile body for interior tiles; kept to bf16 head dims <= 64,
-// where the registers allow it (the head-dim-128 backward with both copies is also beyond what
-// this compiler's AGPR rewrite pass handles).
-#ifndef SA_SPLIT_BODY
-#define SA_SPLIT_BODY 0
-#endif
-template <class OP, int D>
-constexpr bool split_body() { return SA_SPLIT_BODY && sizeof(typename OP::elem) == 2 && D <= 64; }
 
 // ---------------------------------------------------------------------------------------------
 // Backward helpers on (queries x keys) C-layout tiles: lane n holds key j = key0 + n, rows are the
 // queries qbase + crow(i, h), i = 0..15 (h = lane / 32).
 
+// Backward tiles hold (queries x keys) in C layout: lane n is key j, element i is query row
+// qbase + crow(i, h). Rows past the sequence end need no mask here: their Q, dO rows are staged as
+// zeros and their lse as +inf, so their logits, selection, P and dz are all zero. The remaining
+// masks compare the row's offset within its half-wavefront, crow(i, 0), with a per-lane threshold:
+//   P, dz:     j <= r  (and j < T)           <=>  crow(i, 0) >= thr_p = j - qbase - 4h  (32 if j >= T)
+//   selection: j <  r  (and exempt <= j < T) <=>  crow(i, 0) >  thr_s = j - qbase - 4h  (32 if not)
+struct TileMasks {
+  int thr_p, thr_s;
+  __device__ __forceinline__ TileMasks(int j, int qbase, int T, int exempt, int h) {
+    const int d = j - qbase - 4 * h;
+    thr_p = j < T ? d : 32;
+    thr_s = (j < T && j >= exempt) ? d : 32;
+  }
+};
+
 // Head 0's selection on a tile of its raw logits l0, in log2 units: sel = relu(s log2e l0) where
 // exempt <= j < r < T, and the history F[r, j] = hist2 + sum of sel over the tile's earlier rows
-// (the running sum runs down the rows; the half-wavefronts exchange partial sums). Bit i of `gate`
-// is sel[i] > 0, the gate of the gradient path. EDGE (wave-uniform) marks tiles where some pair fails
-// exempt <= j < r < T; elsewhere the gate is the sign of the logit alone.
-template <bool EDGE>
-__device__ __forceinline__ void selection_tile(const f32x16& l0, float hist2, int qbase, int j, int T, int exempt,
-                                               float sl2, int h, f32x16& fs, uint32_t& gate) {
+// (the running sum runs down the rows; the half-wavefronts exchange partial sums). gate[i] is
+// sel[i] > 0, the gate of the gradient path. `edge` (wave-uniform) marks tiles where some pair
+// fails exempt <= j < r: the mask is applied there (every tile when ALWAYS, which costs a few
+// instructions per element but no branch).
+template <bool ALWAYS>
+__device__ __forceinline__ void selection_tile(const f32x16& l0, float hist2, float sl2, int h, bool edge,
+                                               const TileMasks& mk, uint32_t& gate, f32x16& fs) {
   f32x16 sel;
+#pragma unroll
+  for (int i = 0; i < 16; ++i) sel[i] = fmaxf(l0[i] * sl2, 0.f);
+  if (ALWAYS || edge) {
+#pragma unroll
+    for (int i = 0; i < 16; ++i) sel[i] = crow(i, 0) > mk.thr_s ? sel[i] : 0.f;
+  }
   gate = 0;
 #pragma unroll
-  for (int i = 0; i < 16; ++i) {
-    const float sv = l0[i] * sl2;
-    if constexpr (EDGE) {
-      const int r = qbase + crow(i, h);
-      const bool pair = (r < T) && (j >= exempt) && (j < r);
-      sel[i] = (pair && sv > 0.f) ? sv : 0.f;
-    } else {
-      sel[i] = fmaxf(sv, 0.f);
-    }
-    gate |= sel[i] > 0.f ? (1u << i) : 0u;
-  }
+  for (int i = 0; i < 16; ++i) gate |= sel[i] > 0.f ? (1u << i) : 0u;
   float run = hist2;
 #pragma unroll
   for (int a = 0; a < 4; ++a) {
@@ -796,47 +801,65 @@ __device__ __forceinline__ void selection_tile(const f32x16& l0, float hist2, in
 }
 
 // Selection gradient path: U[r, j] = u_in + sum of z over the tile's later rows, and
-// g = -gate U (gate bit i: sel[i] > 0). Returns u_in + the sum over the whole tile (U entering the tile above).
+// g = -U where the gate is set, else 0. Returns u_in + the sum over the whole tile (U entering the
+// tile above). The sum runs negated so the select takes -U without a modifier.
 __device__ __forceinline__ float gpath_tile(const f32x16& z, float u_in, uint32_t gate, int h, f32x16& gp) {
-  float run = u_in;
+  float nrun = -u_in;
 #pragma unroll
   for (int a = 3; a >= 0; --a) {
     const Halves g = halves(((z[4 * a + 3] + z[4 * a + 2]) + z[4 * a + 1]) + z[4 * a]);
-    float p = (h == 1) ? run : run + g.hi;
+    float np = (h == 1) ? nrun : nrun - g.hi;
 #pragma unroll
     for (int t = 3; t >= 0; --t) {
       const int i = 4 * a + t;
-      gp[i] = ((gate >> i) & 1u) ? -p : 0.f;
-      p += z[i];
+      gp[i] = ((gate >> i) & 1u) ? np : 0.f;
+      np -= z[i];
     }
-    run = (run + g.hi) + g.lo;
+    nrun = (nrun - g.hi) - g.lo;
   }
-  return run;
+  return -nrun;
 }
 
 // P = exp2(s log2e lg - F - lse) and dz = P (dp - dbar) on a tile; lse and dbar of the tile's rows
-// come from LDS (4 consecutive rows per float4). MASK (wave-uniform) zeroes pairs outside
-// j <= r < T, j < T.
-template <bool MASK>
+// come from LDS (4 consecutive rows per float4). Pairs outside j <= r, j < T are zeroed on `edge`
+// tiles (every tile when ALWAYS).
+template <bool ALWAYS>
 __device__ __forceinline__ void p_dz_tile(const f32x16& lg, const f32x16& dp, const f32x16& fs, const float* slse,
-                                          const float* sdb, float sl2, int qbase, int j, int T, int h, f32x16& pr,
-                                          f32x16& dz) {
+                                          const float* sdb, float sl2, int h, bool edge, const TileMasks& mk,
+                                          f32x16& pr, f32x16& dz) {
+  if constexpr (ALWAYS) {
 #pragma unroll
-  for (int a = 0; a < 4; ++a) {
-    const float4 ls = *reinterpret_cast<const float4*>(slse + 8 * a + 4 * h);
-    const float4 dbv = *reinterpret_cast<const float4*>(sdb + 8 * a + 4 * h);
-    const float lsv[4] = {ls.x, ls.y, ls.z, ls.w};
-    const float dbs[4] = {dbv.x, dbv.y, dbv.z, dbv.w};
+    for (int a = 0; a < 4; ++a) {
+      const float4 ls = *reinterpret_cast<const float4*>(slse + 8 * a + 4 * h);
+      const float4 dbv = *reinterpret_cast<const float4*>(sdb + 8 * a + 4 * h);
+      const float lsv[4] = {ls.x, ls.y, ls.z, ls.w};
+      const float dbs[4] = {dbv.x, dbv.y, dbv.z, dbv.w};
 #pragma unroll
-    for (int t = 0; t < 4; ++t) {
-      const int i = 4 * a + t;
-      float p = fast_exp2(fmaf(lg[i], sl2, -(fs[i] + lsv[t])));
-      if constexpr (MASK) {
-        const int r = qbase + crow(i, h);
-        p = (j <= r && r < T && j < T) ? p : 0.f;
+      for (int t = 0; t < 4; ++t) {
+        const int i = 4 * a + t;
+        const float p = fast_exp2(fmaf(lg[i], sl2, -(fs[i] + lsv[t])));
+        pr[i] = crow(i, 0) >= mk.thr_p ? p : 0.f;
+        dz[i] = pr[i] * (dp[i] - dbs[t]);
       }
-      pr[i] = p;
-      dz[i] = p * (dp[i] - dbs[t]);
+    }
+  } else {
+#pragma unroll
+    for (int a = 0; a < 4; ++a) {
+      const float4 ls = *reinterpret_cast<const float4*>(slse + 8 * a + 4 * h);
+      const float lsv[4] = {ls.x, ls.y, ls.z, ls.w};
+#pragma unroll
+      for (int t = 0; t < 4; ++t) pr[4 * a + t] = fast_exp2(fmaf(lg[4 * a + t], sl2, -(fs[4 * a + t] + lsv[t])));
+    }
+    if (edge) {
+#pragma unroll
+      for (int i = 0; i < 16; ++i) pr[i] = crow(i, 0) >= mk.thr_p ? pr[i] : 0.f;
+    }
+#pragma unroll
+    for (int a = 0; a < 4; ++a) {
+      const float4 dbv = *reinterpret_cast<const float4*>(sdb + 8 * a + 4 * h);
+      const float dbs[4] = {dbv.x, dbv.y, dbv.z, dbv.w};
+#pragma unroll
+      for (int t = 0; t < 4; ++t) dz[4 * a + t] = pr[4 * a + t] * (dp[4 * a + t] - dbs[t]);
     }
   }
 }
@@ -874,7 +897,6 @@ __global__ __launch_bounds__(NTHREADS, (kv_min_blocks<OP, D, G>())) void bwd_kv_
   constexpr int AS = OP::acc_steps;
   constexpr int NH = G + 1;   // staged heads: the group, then head 0 when outside the group
   constexpr bool KV_PIPE = SA_KV_PIPE != 0;
-  constexpr bool SPLIT_BODY = split_body<OP, D>();
   // two buffers (the tile being computed, the next one being written) when they fit in LDS
   constexpr int TILE_BYTES = (NH * (TILE * LDK + D * LDV) + G * (TILE * LDK + D * LDV)) * (int)sizeof(elem);
   constexpr int NBUF = (KV_PIPE && 2 * TILE_BYTES <= 120 * 1024) ? 2 : 1;
@@ -996,7 +1018,7 @@ __global__ __launch_bounds__(NTHREADS, (kv_min_blocks<OP, D, G>())) void bwd_kv_
       const int r = qbase + (tid & (TILE - 1));
       const int rr = min(r, T - 1);
       const float lv = lse[row * T + rr], dv_ = dbar[row * T + rr];
-      nLse[g] = r < T ? lv : 0.f;
+      nLse[g] = r < T ? lv : INFINITY;   // rows past the end: P = 0
       nDb[g] = r < T ? dv_ : 0.f;
     }
     if (!has_h0) {
@@ -1076,22 +1098,29 @@ __global__ __launch_bounds__(NTHREADS, (kv_min_blocks<OP, D, G>())) void bwd_kv_
     }
     if (qbase + TILE - 1 >= key0) {   // else every query of the tile precedes every key
       if (h == 0 && j < T) uplane[(int64_t)qb * T + j] = ucarry;
-      // tile body; EDGE: some pair of the tile is masked (diagonal, sequence end) or exempt
-      auto body = [&](auto edge_tag) {
-        constexpr bool EDGE = decltype(edge_tag)::value;
+      // tile body; edge: some pair of the tile is masked (diagonal, sequence end) or exempt
+      // (rows past the end and keys past the end need no mask on the key side: the latter's sums
+      // stay in their own lanes, which are never written)
+      const bool edge = (qbase <= key0 + TILE - 1) || key0 < exempt;
+      const TileMasks mk(j, qbase, T, exempt, h);
+      // (a lambda: inlined late, its loop-invariant parts are not hoisted out of the tile loop,
+      // which would hold them in registers across it)
+      auto body = [&]() {
         const elem* q0s = has_h0 ? sQ[buf][0] : sQ[buf][G];
         f32x16 l0 = zero16();
 #pragma unroll
         for (int s = 0; s < NS; ++s) l0 = OP::mma(OP::ld_std(q0s, LDK, n, h, s), k0_frag(s), l0);
         f32x16 fs;
         uint32_t gate;
-        selection_tile<EDGE>(l0, (j < T) ? hist * LOG2E : 0.f, qbase, j, T, exempt, sl2, h, fs, gate);
+        selection_tile<true>(l0, (j < T) ? hist * LOG2E : 0.f, sl2, h, edge, mk, gate, fs);
 
+        // Per head: P and dz, dV^T += dO^T P, dK^T += Q^T dz; then g from the group's dz sum goes to
+        // head 0's dK: added to head 0's own dz when the group holds it, else into dk0t.
         f32x16 dzsum, dz0;
 #pragma unroll
         for (int g = 0; g < G; ++g) {
           f32x16 lg;
-          if (has_h0 && g == 0) {   // head 0 itself: its logits are l0, its dK waits for g
+          if (has_h0 && g == 0) {   // head 0 itself: its logits are l0
             lg = l0;
           } else {
             lg = zero16();
@@ -1102,35 +1131,28 @@ __global__ __launch_bounds__(NTHREADS, (kv_min_blocks<OP, D, G>())) void bwd_kv_
 #pragma unroll
           for (int s = 0; s < NS; ++s) dp = OP::mma(OP::ld_std(sdO[buf][g], LDK, n, h, s), v_frag(g, s), dp);
           f32x16 pr, dz;
-          p_dz_tile<EDGE>(lg, dp, fs, sLse[buf][g], sDb[buf][g], sl2, qbase, j, T, h, pr, dz);
-          acc_t(dvt[g], sdOt[buf][g], pr, split_keys);   // dV^T += dO^T P
+          p_dz_tile<true>(lg, dp, fs, sLse[buf][g], sDb[buf][g], sl2, h, edge, mk, pr, dz);
+          acc_t(dvt[g], sdOt[buf][g], pr, split_keys);
           if (g == 0) {
             dzsum = dz;
           } else {
 #pragma unroll
             for (int i = 0; i < 16; ++i) dzsum[i] += dz[i];
           }
-          if (has_h0 && g == 0) {
-            dz0 = dz;
-          } else {
-            acc_t(dkt[g], sQt[buf][g], dz, split_keys);   // dK^T += Q^T dz
-          }
+          if (has_h0 && g == 0) dz0 = dz;   // head 0's dK waits for g
+          else acc_t(dkt[g], sQt[buf][g], dz, split_keys);
         }
-
         f32x16 gp;
         ucarry = gpath_tile(dzsum, ucarry, gate, h, gp);
         if (has_h0) {
-          f32x16 dzh;
 #pragma unroll
-          for (int i = 0; i < 16; ++i) dzh[i] = dz0[i] + gp[i];
-          acc_t(dkt[0], sQt[buf][0], dzh, true);
+          for (int i = 0; i < 16; ++i) dz0[i] += gp[i];
+          acc_t(dkt[0], sQt[buf][0], dz0, true);
         } else {
           acc_t(dk0t, sQt[buf][G], gp, big_tile(gp));
         }
       };
-      const bool edge = (qbase <= key0 + TILE - 1) || (qbase + TILE > T) || (key0 + TILE > T) || key0 < exempt;
-      if (!SPLIT_BODY || edge) body(std::true_type{});   // the masked body is right on every tile
-      else body(std::false_type{});
+      body();
     }
     if constexpr (KV_PIPE) {
       if constexpr (NBUF == 1) __syncthreads();   // the one buffer is free again
@@ -1191,7 +1213,6 @@ __global__ __launch_bounds__(NTHREADS, (dq_min_blocks<OP, D>())) void bwd_dq_ker
   constexpr int AS = OP::acc_steps;
   constexpr int NH = G + 1;
   constexpr bool DQ_PIPE = SA_DQ_PIPE != 0;
-  constexpr bool SPLIT_BODY = split_body<OP, D>();
   constexpr int TILE_BYTES = (NH * (TILE * LDK + D * LDKT) + G * TILE * LDK) * (int)sizeof(elem);
   constexpr int NBUF = (DQ_PIPE && 2 * TILE_BYTES <= 120 * 1024) ? 2 : 1;
 
@@ -1273,7 +1294,7 @@ __global__ __launch_bounds__(NTHREADS, (dq_min_blocks<OP, D>())) void bwd_dq_ker
     const int64_t row = seq_row + hd0 + g;
     if (lane < TILE) {
       const int r = qbase + lane;
-      sLse[wave][g][lane] = (r < T) ? lse[row * T + r] : 0.f;
+      sLse[wave][g][lane] = (r < T) ? lse[row * T + r] : INFINITY;   // rows past the end: P = 0
       sDb[wave][g][lane] = (r < T) ? dbar[row * T + r] : 0.f;
     }
   }
@@ -1387,8 +1408,10 @@ __global__ __launch_bounds__(NTHREADS, (dq_min_blocks<OP, D>())) void bwd_dq_ker
     }
     if (ktile < my_end) {
       const int j = kbase + n;
-      auto body = [&](auto edge_tag) {
-        constexpr bool EDGE = decltype(edge_tag)::value;
+      // tile body; edge: some pair of the tile is masked (diagonal, sequence end) or exempt
+      const bool edge = (kbase + TILE - 1 >= qbase) || (kbase + TILE > T) || kbase < exempt;
+      const TileMasks mk(j, qbase, T, exempt, h);
+      {
         const elem* k0s = has_h0 ? sK[buf][0] : sK[buf][G];
         f32x16 l0 = zero16();
 #pragma unroll
@@ -1396,14 +1419,13 @@ __global__ __launch_bounds__(NTHREADS, (dq_min_blocks<OP, D>())) void bwd_dq_ker
           l0 = OP::mma(has_h0 ? q_frag(0, s) : q0a[s], OP::ld_std(k0s, LDK, n, h, s), l0);
         f32x16 fs;
         uint32_t gate;
-        selection_tile<EDGE>(l0, hist * LOG2E, qbase, j, T, exempt, sl2, h, fs, gate);
+        selection_tile<false>(l0, hist * LOG2E, sl2, h, edge, mk, gate, fs);
 
         f32x16 zsum, dz0;
 #pragma unroll
-        for (int gg = 0; gg < G; ++gg) {
-          const int g = has_h0 ? (gg + 1) % G : gg;
+        for (int g = 0; g < G; ++g) {
           f32x16 lg;
-          if (has_h0 && g == 0) {
+          if (has_h0 && g == 0) {   // head 0 itself: its logits are l0, its dQ waits for g
             lg = l0;
           } else {
             lg = zero16();
@@ -1416,8 +1438,8 @@ __global__ __launch_bounds__(NTHREADS, (dq_min_blocks<OP, D>())) void bwd_dq_ker
           for (int s = 0; s < NS; ++s)
             dp = OP::mma(do_frag(g, s), OP::ld_std(sV[buf][g], LDK, n, h, s), dp);
           f32x16 pr, dz;
-          p_dz_tile<EDGE>(lg, dp, fs, sLse[wave][g], sDb[wave][g], sl2, qbase, j, T, h, pr, dz);
-          if (gg == 0) {
+          p_dz_tile<false>(lg, dp, fs, sLse[wave][g], sDb[wave][g], sl2, h, edge, mk, pr, dz);
+          if (g == 0) {
             zsum = dz;
           } else {
 #pragma unroll
@@ -1440,10 +1462,7 @@ __global__ __launch_bounds__(NTHREADS, (dq_min_blocks<OP, D>())) void bwd_dq_ker
         } else {
           acc_xk(dq0acc, gp, sKt[buf][G], big_tile(gp));
         }
-      };
-      const bool edge = (kbase + TILE - 1 >= qbase) || (qbase + TILE > T) || (kbase + TILE > T) || kbase < exempt;
-      if (!SPLIT_BODY || edge) body(std::true_type{});   // the masked body is right on every tile
-      else body(std::false_type{});
+      }
     }
     if constexpr (DQ_PIPE) {
       if constexpr (NBUF == 1) __syncthreads();   // the one buffer is free again
