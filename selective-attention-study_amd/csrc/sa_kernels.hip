@@ -249,10 +249,12 @@ __device__ __forceinline__ void stage_cols(E* s, const E* g, int64_t gld, int co
 }
 
 // Unpadded LDS rows of 64 bf16 (eight 16-byte chunks), chunk c of row r stored at chunk position
-// (c + r + r/8) mod 8. A lane-per-row fragment read (every lane the same logical chunk) then puts
-// any 8 aligned consecutive rows on 8 distinct 16-byte bank groups and any 16 on 16 distinct
-// (32 or 64 four-byte banks), as a padded row stride would, without the padding's bytes.
-__device__ __forceinline__ int swz64(int r, int c) { return r * 64 + (((c + r + (r >> 3)) & 7) << 3); }
+// (c + r/2) mod 8. A 16-byte read serves 16 lanes per pass from 64 four-byte banks (256 bytes):
+// two consecutive 128-byte rows already fall in different halves, and the rotation by r/2 puts the
+// eight row pairs of a pass on distinct chunks, so a lane-per-row fragment read (every lane the
+// same logical chunk) is conflict-free, as with a padded row stride, without the padding's bytes
+// (measured: a rotation by r or an XOR by r mod 8 takes twice the cycles).
+__device__ __forceinline__ int swz64(int r, int c) { return r * 64 + (((c + (r >> 1)) & 7) << 3); }
 
 // Register-staged tiles for software pipelining: load() issues a tile's global loads into registers
 // (each thread owns PER 16-byte chunks), store() later writes them to LDS, so the loads of the next
@@ -441,8 +443,16 @@ __global__ __launch_bounds__(NTHREADS) void sel_scan_kernel(
 // tiles rarely trigger a rescale of the output (skipped when no lane's maximum rises). The next
 // tile's K, V^T and carry rows are loaded while the current one is computed (double-buffered LDS).
 
+// Workgroups per CU the forward's register allocation must allow: three at bf16 head dims <= 64
+// (its LDS fits three), which holds it to 168 registers without spills.
+#ifndef SA_FWD_MIN_BLOCKS
+#define SA_FWD_MIN_BLOCKS 3
+#endif
 template <class OP, int D, int G>
-__global__ __launch_bounds__(NTHREADS) void fwd_kernel(
+constexpr int fwd_min_blocks() { return (sizeof(typename OP::elem) == 2 && D <= 64 && G == 1) ? SA_FWD_MIN_BLOCKS : 1; }
+
+template <class OP, int D, int G>
+__global__ __launch_bounds__(NTHREADS, (fwd_min_blocks<OP, D, G>())) void fwd_kernel(
     const typename OP::elem* __restrict__ q, const typename OP::elem* __restrict__ k,
     const typename OP::elem* __restrict__ vt, const float* __restrict__ carry,
     float* __restrict__ out, float* __restrict__ rmax, float* __restrict__ rden,
@@ -462,6 +472,8 @@ __global__ __launch_bounds__(NTHREADS) void fwd_kernel(
   __shared__ __attribute__((aligned(16))) elem sK[NBUF][NH][TILE * LDK];
   __shared__ __attribute__((aligned(16))) elem sVt[NBUF][G][D * LDV];
   __shared__ __attribute__((aligned(16))) float sC[NBUF][NWAVES][TILE];   // carry rows, log2 units
+  constexpr int LDF = TILE + 4;
+  __shared__ __attribute__((aligned(16))) float sF[NWAVES][TILE * LDF];   // each wavefront's F tile
 
   const int tid = threadIdx.x, lane = tid & 63, wave = wave_id();
   const int n = lane & 31, h = lane >> 5;
@@ -557,33 +569,51 @@ __global__ __launch_bounds__(NTHREADS) void fwd_kernel(
       const int kbase = kt * TILE;
       auto body = [&](auto edge_tag) {
         constexpr bool EDGE = decltype(edge_tag)::value;
-        // head 0 logits (keys x queries) -> selection (log2 units) -> F
-        f32x16 l0 = zero16();
+        // Head 0's logits as (queries x keys), lane = key kbase + n: the selection's running sum
+        // over queries then stays within the lane. F (log2 units) = the carry at the block's first
+        // query + the selection by the block's earlier queries; it returns to the (keys x queries)
+        // layout of the softmax through this wavefront's LDS rows.
+        f32x16 l0t = zero16();
         {
           const elem* k0s = has_h0 ? sK[buf][0] : sK[buf][G];
 #pragma unroll
           for (int s = 0; s < NS; ++s)
-            l0 = OP::mma(OP::ld_std(k0s, LDK, n, h, s), has_h0 ? qf[0][s] : q0f[s], l0);
+            l0t = OP::mma(has_h0 ? qf[0][s] : q0f[s], OP::ld_std(k0s, LDK, n, h, s), l0t);
         }
-        f32x16 fs;
+        {
+          f32x16 sel;
 #pragma unroll
-        for (int i = 0; i < 16; ++i) {
-          const float sv = l0[i] * sl2;
+          for (int i = 0; i < 16; ++i) sel[i] = fmaxf(l0t[i] * sl2, 0.f);
           if constexpr (EDGE) {
-            const int j = kbase + crow(i, h);
-            fs[i] = (j >= exempt && j < q_abs && sv > 0.f) ? sv : 0.f;
-          } else {
-            fs[i] = fmaxf(sv, 0.f);
+            // pairs exempt <= j < r; keys past the end and queries past the end hold zero rows
+            const int jk = kbase + n;
+            const int thr = jk >= exempt ? jk - (q_off + rb * TILE) - 4 * h : 32;
+#pragma unroll
+            for (int i = 0; i < 16; ++i) sel[i] = crow(i, 0) > thr ? sel[i] : 0.f;
+          }
+          float run = sC[buf][wave][n];
+          float* fw = sF[wave];
+#pragma unroll
+          for (int a = 0; a < 4; ++a) {
+            const Halves g = halves(((sel[4 * a] + sel[4 * a + 1]) + sel[4 * a + 2]) + sel[4 * a + 3]);
+            float p = (h == 0) ? run : run + g.lo;   // rows 8a..8a+3 in the low half, 8a+4.. in the high
+#pragma unroll
+            for (int t = 0; t < 4; ++t) {
+              fw[crow(4 * a + t, h) * LDF + n] = p;
+              p += sel[4 * a + t];
+            }
+            run = (run + g.lo) + g.hi;
           }
         }
-        excl_scan32x16(fs);   // selection by the block's earlier queries
+        lds_wave_sync();
+        f32x16 fs;
 #pragma unroll
         for (int a = 0; a < 4; ++a) {
-          const float4 c4 = *reinterpret_cast<const float4*>(&sC[buf][wave][8 * a + 4 * h]);
-          fs[4 * a] += c4.x;
-          fs[4 * a + 1] += c4.y;
-          fs[4 * a + 2] += c4.z;
-          fs[4 * a + 3] += c4.w;
+          const float4 f4 = *reinterpret_cast<const float4*>(&sF[wave][n * LDF + 8 * a + 4 * h]);
+          fs[4 * a] = f4.x;
+          fs[4 * a + 1] = f4.y;
+          fs[4 * a + 2] = f4.z;
+          fs[4 * a + 3] = f4.w;
         }
         if (damp_mode != 0) {
 #pragma unroll
@@ -592,14 +622,9 @@ __global__ __launch_bounds__(NTHREADS) void fwd_kernel(
 
 #pragma unroll
         for (int g = 0; g < G; ++g) {
-          f32x16 lg;
-          if (g == 0 && has_h0) {
-            lg = l0;
-          } else {
-            lg = zero16();
+          f32x16 lg = zero16();
 #pragma unroll
-            for (int s = 0; s < NS; ++s) lg = OP::mma(OP::ld_std(sK[buf][g], LDK, n, h, s), qf[g][s], lg);
-          }
+          for (int s = 0; s < NS; ++s) lg = OP::mma(OP::ld_std(sK[buf][g], LDK, n, h, s), qf[g][s], lg);
           float zmax = -INFINITY;
 #pragma unroll
           for (int i = 0; i < 16; ++i) {
