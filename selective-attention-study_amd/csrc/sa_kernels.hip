@@ -248,6 +248,25 @@ __device__ __forceinline__ void stage_cols(E* s, const E* g, int64_t gld, int co
   }
 }
 
+// The dispatcher deals workgroups round-robin to the 8 XCDs, each with its own L2. The attention
+// kernels remap the linear workgroup id so that every XCD takes a contiguous range of the
+// (head group, block) order instead: the workgroups one L2 serves at a time then belong to one or
+// two heads and share that head's tiles.
+#ifndef SA_XCD_REMAP
+#define SA_XCD_REMAP 1
+#endif
+constexpr int NXCD = 8;
+struct BlockXY {
+  int x, y;
+};
+__device__ __forceinline__ BlockXY xcd_block() {
+  const int gx = gridDim.x, n = gx * gridDim.y;
+  const int l = blockIdx.x + gx * blockIdx.y;
+  const int per = n / NXCD;
+  const int m = (SA_XCD_REMAP && l < per * NXCD) ? (l % NXCD) * per + l / NXCD : l;
+  return {m % gx, m / gx};
+}
+
 // Unpadded LDS rows of 64 bf16 (eight 16-byte chunks), chunk c of row r stored at chunk position
 // (c + r/2) mod 8. A 16-byte read serves 16 lanes per pass from 64 four-byte banks (256 bytes):
 // two consecutive 128-byte rows already fall in different halves, and the rotation by r/2 puts the
@@ -478,12 +497,13 @@ __global__ __launch_bounds__(NTHREADS, (fwd_min_blocks<OP, D, G>())) void fwd_ke
   const int tid = threadIdx.x, lane = tid & 63, wave = wave_id();
   const int n = lane & 31, h = lane >> 5;
   const int groups = H / G;
-  const int b = blockIdx.y / groups, gi = blockIdx.y % groups;
+  const BlockXY bxy = xcd_block();
+  const int b = bxy.y / groups, gi = bxy.y % groups;
   const int hd0 = gi * G;
   const bool has_h0 = (gi == 0);
   const int NBq = (Tq + TILE - 1) / TILE;
   const int NKT = (Tk + TILE - 1) / TILE;
-  const int qsb = gridDim.x - 1 - blockIdx.x;
+  const int qsb = gridDim.x - 1 - bxy.x;
   const int rb = qsb * NWAVES + wave;
   const int q_rel = rb * TILE + n;
   const int q_abs = q_off + q_rel;
@@ -943,11 +963,12 @@ __global__ __launch_bounds__(NTHREADS, (kv_min_blocks<OP, D, G>())) void bwd_kv_
   const int tid = threadIdx.x, lane = tid & 63, wave = wave_id();
   const int n = lane & 31, h = lane >> 5;
   const int groups = H / G;
-  const int b = blockIdx.y / groups, gi = blockIdx.y % groups;
+  const BlockXY bxy = xcd_block();
+  const int b = bxy.y / groups, gi = bxy.y % groups;
   const int hd0 = gi * G;
   const bool has_h0 = (gi == 0);
   const int NB = (T + TILE - 1) / TILE;
-  const int key0 = blockIdx.x * (NWAVES * TILE) + wave * TILE;
+  const int key0 = bxy.x * (NWAVES * TILE) + wave * TILE;
   const int j = key0 + n;
   const int64_t seq_row = (int64_t)b * H;
   float* uplane = ucheck + ((int64_t)gi * nseq + b) * NB * (int64_t)T;
@@ -1024,7 +1045,7 @@ __global__ __launch_bounds__(NTHREADS, (kv_min_blocks<OP, D, G>())) void bwd_kv_
   float ucarry = 0.f;
   const float sl2 = scale * LOG2E;
   // query tiles the workgroup visits, last to first: NB-1 down to the first that reaches its keys
-  const int qb_lo = blockIdx.x * NWAVES;
+  const int qb_lo = bxy.x * NWAVES;
   const int ntiles = NB - qb_lo;
 
   // Staging of one query tile: Q, Q^T, dO, dO^T of the group (+ head 0's Q, Q^T), lse, dbar.
@@ -1258,11 +1279,12 @@ __global__ __launch_bounds__(NTHREADS, (dq_min_blocks<OP, D>())) void bwd_dq_ker
   const int tid = threadIdx.x, lane = tid & 63, wave = wave_id();
   const int n = lane & 31, h = lane >> 5;
   const int groups = H / G;
-  const int b = blockIdx.y / groups, gi = blockIdx.y % groups;
+  const BlockXY bxy = xcd_block();
+  const int b = bxy.y / groups, gi = bxy.y % groups;
   const int hd0 = gi * G;
   const bool has_h0 = (gi == 0);
   const int NB = (T + TILE - 1) / TILE;
-  const int qsb = gridDim.x - 1 - blockIdx.x;
+  const int qsb = gridDim.x - 1 - bxy.x;
   const int qb = qsb * NWAVES + wave;
   const int qbase = qb * TILE;
   const int64_t seq_row = (int64_t)b * H;
