@@ -1,13 +1,35 @@
 #!/usr/bin/env bash
-# Builds libsa_hip.so (gfx950) next to the Python package. Run from anywhere.
+# Builds libsa_hip.so (gfx950) next to the Python package. Run from anywhere; extra arguments are
+# passed to every compile (e.g. -DSA_FWD_MIN_BLOCKS=2). SA_OUT overrides the output path.
+#
+# Translation units, compiled in parallel:
+#   sa_bf16.hip  bf16-storage kernels, -amdgpu-mfma-vgpr-form: MFMA accumulators in VGPRs (left to
+#                its heuristics the compiler keeps them in AGPRs and copies every loop-carried
+#                accumulator back and forth each iteration)
+#   sa_f32.hip   fp32-storage kernels, the compiler's own accumulator placement
+#   sa_abi.hip   the C ABI (host code only)
+# Every HIP compile: -packed-fp32-ops off (no v_pk_*_f32 from the compiler).
 set -euo pipefail
 here="$(cd "$(dirname "${BASH_SOURCE[0]}")" && pwd)"
 root="$(cd "$here/../.." && pwd)"
 out="${SA_OUT:-$here/../selective_attention/libsa_hip.so}"
-# -amdgpu-mfma-vgpr-form: MFMA accumulators live in VGPRs; left to its heuristics the compiler keeps
-# them in AGPRs and copies every loop-carried accumulator back and forth each iteration.
-hipcc --offload-arch=gfx950 -O3 -std=c++17 -fPIC -shared -munsafe-fp-atomics \
-  -Xclang -target-feature -Xclang -packed-fp32-ops -mllvm -amdgpu-mfma-vgpr-form \
-  "$@" -I"$root/include" "$here/sa_kernels.hip" -o "$out.tmp"
+tmp="$(mktemp -d)"
+trap 'rm -rf "$tmp"' EXIT
+
+common=(--offload-arch=gfx950 -O3 -std=c++17 -fPIC -munsafe-fp-atomics
+        -Xclang -target-feature -Xclang -packed-fp32-ops -I"$root/include" "$@")
+
+hipcc "${common[@]}" -mllvm -amdgpu-mfma-vgpr-form -c "$here/sa_bf16.hip" -o "$tmp/sa_bf16.o" &
+p1=$!
+hipcc "${common[@]}" -c "$here/sa_f32.hip" -o "$tmp/sa_f32.o" &
+p2=$!
+hipcc "${common[@]}" -c "$here/sa_abi.hip" -o "$tmp/sa_abi.o" &
+p3=$!
+rc=0
+wait $p1 || rc=1
+wait $p2 || rc=1
+wait $p3 || rc=1
+[ $rc -eq 0 ] || { echo "build.sh: a compile failed" >&2; exit 1; }
+hipcc --offload-arch=gfx950 -shared -fPIC "$tmp/sa_bf16.o" "$tmp/sa_f32.o" "$tmp/sa_abi.o" -o "$out.tmp"
 mv "$out.tmp" "$out"
 echo "built $out"

@@ -1,0 +1,123 @@
+// The C ABI of libsa_hip.so (include/sa.h): argument checks, workspace sizes, the timing
+// registry, and dispatch to the bf16 / fp32 translation units.
+
+#include <math.h>
+
+#include "sa_host.h"
+
+namespace sa_host {
+
+TimingRegistry& timing() {
+  static TimingRegistry r;
+  return r;
+}
+
+}  // namespace sa_host
+
+using namespace sa_host;
+
+// ---------------------------------------------------------------------------------------------
+// C ABI
+
+extern "C" {
+
+int sa_abi_version(void) { return 2; }
+
+int sa_timing_enable(int on) {
+  TimingRegistry& r = timing();
+  std::lock_guard<std::mutex> lock(r.mu);
+  for (auto& list : r.events) {
+    for (auto& ev : list) {
+      (void)hipEventDestroy(ev.first);
+      (void)hipEventDestroy(ev.second);
+    }
+    list.clear();
+  }
+  r.on = on != 0;
+  return SA_OK;
+}
+
+int sa_timing_read(int kernel, double* total_ms, int64_t* launches) {
+  if (kernel < 0 || kernel >= SA_KERNEL_COUNT || !total_ms || !launches) return SA_ERR_ARGUMENT;
+  TimingRegistry& r = timing();
+  std::lock_guard<std::mutex> lock(r.mu);
+  double sum = 0.0;
+  for (auto& ev : r.events[kernel]) {
+    float ms = 0.f;
+    if (hipEventSynchronize(ev.second) != hipSuccess || hipEventElapsedTime(&ms, ev.first, ev.second) != hipSuccess)
+      return SA_ERR_LAUNCH;
+    sum += ms;
+  }
+  *total_ms = sum;
+  *launches = (int64_t)r.events[kernel].size();
+  return SA_OK;
+}
+
+const char* sa_status_string(int status) {
+  switch (status) {
+    case SA_OK: return "ok";
+    case SA_ERR_ARGUMENT: return "invalid argument (size, pointer or option)";
+    case SA_ERR_HEAD_DIM: return "head_dim must be 32, 64 or 128 at the C ABI";
+    case SA_ERR_DTYPE: return "unknown dtype code";
+    case SA_ERR_WORKSPACE: return "workspace too small";
+    case SA_ERR_LAUNCH: return "HIP kernel launch failed";
+    default: return "unknown status";
+  }
+}
+
+int64_t sa_transposed_ld(int64_t t) { return align_up(t < 1 ? 1 : t, 64); }
+
+int64_t sa_forward_workspace_bytes(int64_t nseq, int64_t heads, int64_t tk, int64_t head_dim, int dtype) {
+  const int64_t es = dtype == SA_DTYPE_BF16 ? 2 : 4;
+  return align_up(nseq * heads * head_dim * sa_transposed_ld(tk) * es, 256);
+}
+
+int sa_forward(const void* q, const void* k, const void* v, float* out, float* rmax, float* rden, float* carry,
+               const float* state_in, float* state_out, int64_t state_ld, void* workspace,
+               int64_t workspace_bytes, int64_t nseq, int64_t heads, int64_t tq, int64_t tk, int64_t q_offset,
+               int64_t kv_stride, int64_t head_dim, float scale, int dtype, int exempt, int group, int damp_mode,
+               int64_t train_len, void* stream) {
+  if (!valid_dims(nseq, heads, tk) || tq < 1 || q_offset < 0 || q_offset + tq != tk) return SA_ERR_ARGUMENT;
+  if (kv_stride == 0) kv_stride = tk * head_dim;
+  if (kv_stride < tk * head_dim || kv_stride % 8 != 0) return SA_ERR_ARGUMENT;
+  if (!q || !k || !v || !out || !rmax || !rden || !carry || !state_out || !workspace) return SA_ERR_ARGUMENT;
+  if (q_offset > 0 && !state_in) return SA_ERR_ARGUMENT;
+  if (state_ld < tk || exempt < 1 || damp_mode < 0 || damp_mode > 2 || (damp_mode && train_len < 1))
+    return SA_ERR_ARGUMENT;
+  if (!(scale > 0.f) || !(scale < INFINITY)) return SA_ERR_ARGUMENT;
+  if (dtype != SA_DTYPE_BF16 && dtype != SA_DTYPE_F32) return SA_ERR_DTYPE;
+  if (head_dim != 32 && head_dim != 64 && head_dim != 128) return SA_ERR_HEAD_DIM;
+  if (workspace_bytes < sa_forward_workspace_bytes(nseq, heads, tk, head_dim, dtype)) return SA_ERR_WORKSPACE;
+  const FwdCall c{q,         k,     v,       out,          rmax,        rden,     carry,
+                  state_in,  state_out,    state_ld,     workspace,   (int)nseq, (int)heads, (int)tq,
+                  (int)tk,   kv_stride,    (int)q_offset, scale,      exempt,    group,      damp_mode,
+                  (float)train_len,        (int)head_dim, static_cast<hipStream_t>(stream)};
+  return dtype == SA_DTYPE_BF16 ? forward_bf16(c) : forward_f32(c);
+}
+
+int64_t sa_backward_workspace_bytes(int64_t nseq, int64_t heads, int64_t t, int64_t head_dim, int dtype, int group) {
+  if (!valid_dims(nseq, heads, t) || (dtype != SA_DTYPE_BF16 && dtype != SA_DTYPE_F32)) return -1;
+  return bwd_layout(nseq, heads, t, head_dim, dtype == SA_DTYPE_BF16 ? 2 : 4, bwd_group(dtype, head_dim, heads, group))
+      .total;
+}
+
+int sa_backward(const void* q, const void* k, const void* v, const float* out, const void* dout, const float* rmax,
+                const float* rden, const float* carry, void* dq, void* dk, void* dv, void* workspace,
+                int64_t workspace_bytes, int64_t nseq, int64_t heads, int64_t t, int64_t head_dim, float scale,
+                int dtype, int grad_dtype, int exempt, int group, void* stream) {
+  if (!valid_dims(nseq, heads, t) || exempt < 1) return SA_ERR_ARGUMENT;
+  if (!(scale > 0.f) || !(scale < INFINITY)) return SA_ERR_ARGUMENT;
+  if (!q || !k || !v || !out || !dout || !rmax || !rden || !carry || !dq || !dk || !dv || !workspace)
+    return SA_ERR_ARGUMENT;
+  if (dtype != SA_DTYPE_BF16 && dtype != SA_DTYPE_F32) return SA_ERR_DTYPE;
+  if (grad_dtype != SA_DTYPE_BF16 && grad_dtype != SA_DTYPE_F32) return SA_ERR_DTYPE;
+  if (head_dim != 32 && head_dim != 64 && head_dim != 128) return SA_ERR_HEAD_DIM;
+  if (group < 0 || workspace_bytes < sa_backward_workspace_bytes(nseq, heads, t, head_dim, dtype, group))
+    return SA_ERR_WORKSPACE;
+  const BwdCall c{q,  k,  v,  out, dout, rmax, rden, carry, dq, dk, dv, workspace, (int)nseq, (int)heads, (int)t,
+                  scale, exempt, group, grad_dtype, (int)head_dim, static_cast<hipStream_t>(stream)};
+  return dtype == SA_DTYPE_BF16 ? backward_bf16(c) : backward_f32(c);
+}
+
+}  // extern "C"
+

@@ -1,0 +1,166 @@
+// Host-side pieces shared by the translation units of libsa_hip.so (sa_abi.hip, sa_bf16.hip,
+// sa_f32.hip): tile geometry, head grouping, workspace layout, argument checks, launch timing, and
+// the entry points of the two storage dtypes, which live in their own translation units so that
+// each is compiled with the code-generation options that suit it.
+
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include <mutex>
+#include <utility>
+#include <vector>
+
+#include "sa.h"
+
+#define SA_HIDDEN __attribute__((visibility("hidden")))
+
+namespace sa_host {
+
+constexpr int TILE = 32;      // tile edge and carry checkpoint spacing (queries)
+constexpr int NTHREADS = 256;
+constexpr int NWAVES = 4;
+
+// Event timing of the main kernels, for measurement tools (sa_timing_enable / sa_timing_read).
+// Off by default; when on, each timed launch is bracketed by a pair of HIP events recorded on the
+// launch's own stream. The registry is the only mutable host state of the library.
+struct TimingRegistry {
+  std::mutex mu;
+  bool on = false;
+  std::vector<std::pair<hipEvent_t, hipEvent_t>> events[SA_KERNEL_COUNT];
+};
+TimingRegistry& timing();   // the one registry (sa_abi.hip)
+
+// Brackets one launch: construct before it, destroy after it (both on stream st).
+class TimedLaunch {
+ public:
+  TimedLaunch(int kernel, hipStream_t st) : kernel_(kernel), st_(st) {
+    TimingRegistry& r = timing();
+    std::lock_guard<std::mutex> lock(r.mu);
+    if (!r.on) return;
+    if (hipEventCreate(&start_) != hipSuccess) return;
+    if (hipEventCreate(&stop_) != hipSuccess) {
+      (void)hipEventDestroy(start_);
+      return;
+    }
+    active_ = hipEventRecord(start_, st_) == hipSuccess;
+  }
+  ~TimedLaunch() {
+    if (!active_) return;
+    TimingRegistry& r = timing();
+    std::lock_guard<std::mutex> lock(r.mu);
+    if (hipEventRecord(stop_, st_) == hipSuccess) r.events[kernel_].emplace_back(start_, stop_);
+  }
+
+ private:
+  int kernel_;
+  hipStream_t st_;
+  hipEvent_t start_ = nullptr, stop_ = nullptr;
+  bool active_ = false;
+};
+
+inline int64_t align_up(int64_t x, int64_t a) { return (x + a - 1) / a * a; }
+inline int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
+
+inline int launch_status() { return hipGetLastError() == hipSuccess ? SA_OK : SA_ERR_LAUNCH; }
+
+#ifndef SA_FWD_GROUP_D64
+#define SA_FWD_GROUP_D64 1
+#endif
+inline int auto_group(int dtype, int64_t D, int64_t heads, int requested, bool backward) {
+  int g = requested;
+  if (g <= 0) {
+    if (dtype == SA_DTYPE_F32) g = 1;
+    else if (backward) g = (D <= 32) ? 2 : 1;
+    else g = (D <= 32) ? 4 : (D <= 64 ? SA_FWD_GROUP_D64 : 1);
+  }
+  int cap = (dtype == SA_DTYPE_F32) ? 1 : (backward ? 2 : 4);
+  if (D >= 128 || (backward && D >= 64)) cap = 1;
+  g = g > cap ? cap : g;
+  while (g > 1 && (heads % g != 0)) g >>= 1;
+  return g < 1 ? 1 : g;
+}
+
+// Heads per wavefront of the backward kernels: a group shares head 0's selection work (its logits,
+// the history F and the g products), so wider groups amortise it, within the register budget.
+#ifndef SA_BWD_GROUP_DEFAULT
+#define SA_BWD_GROUP_DEFAULT 1
+#endif
+inline int bwd_group(int dtype, int64_t D, int64_t heads, int requested) {
+  int g = requested > 0 ? requested : SA_BWD_GROUP_DEFAULT;
+  const int cap = (dtype == SA_DTYPE_BF16 && D <= 32) ? 2 : 1;
+  g = g > cap ? cap : g;
+  while (g > 1 && (heads % g != 0)) g >>= 1;
+  return g < 1 ? 1 : g;
+}
+
+struct BwdLayout {
+  int64_t qt, dot, kt, lse, dbar, dq, dk, dv, dq0x, dk0x, ucheck, total;
+};
+
+// Workspace of sa_backward: transposed Q, dO, K; row statistics; fp32 gradient sums; head 0's
+// shares from other groups; the selection-suffix checkpoints (one plane per head group).
+inline BwdLayout bwd_layout(int64_t nseq, int64_t heads, int64_t t, int64_t D, int64_t esize, int64_t G) {
+  const int64_t R = nseq * heads, ldt = sa_transposed_ld(t), NB = (t + TILE - 1) / TILE;
+  BwdLayout L;
+  int64_t off = 0;
+  auto take = [&](int64_t bytes) { int64_t o = off; off = align_up(off + bytes, 256); return o; };
+  L.qt = take(R * D * ldt * esize);
+  L.dot = take(R * D * ldt * esize);
+  L.kt = take(R * D * ldt * esize);
+  L.lse = take(R * t * 4);
+  L.dbar = take(R * t * 4);
+  L.dq = take(R * t * D * 4);
+  L.dk = take(R * t * D * 4);
+  L.dv = take(R * t * D * 4);
+  L.dq0x = take(nseq * t * D * 4);
+  L.dk0x = take(nseq * t * D * 4);
+  L.ucheck = take((heads / G) * nseq * NB * t * 4);
+  L.total = off;
+  return L;
+}
+
+inline bool valid_dims(int64_t nseq, int64_t heads, int64_t t) {
+  const int64_t lim = (int64_t)1 << 30;
+  return nseq >= 1 && heads >= 1 && t >= 1 && nseq < 65536 && heads < 65536 && t < lim && nseq * heads < 65536;
+}
+
+
+// One sa_forward call after its checks (pointers already typed by the storage dtype's entry).
+struct FwdCall {
+  const void *q, *k, *v;
+  float *out, *rmax, *rden, *carry;
+  const float* state_in;
+  float* state_out;
+  int64_t state_ld;
+  void* ws;
+  int nseq, H, Tq, Tk;
+  int64_t kvs;
+  int q_off;
+  float scale;
+  int exempt, group, damp_mode;
+  float train_len;
+  int head_dim;
+  hipStream_t st;
+};
+
+// One sa_backward call after its checks.
+struct BwdCall {
+  const void *q, *k, *v;
+  const float* out;
+  const void* dout;
+  const float *rmax, *rden, *carry;
+  void *dq, *dk, *dv, *ws;
+  int nseq, H, T;
+  float scale;
+  int exempt, group, grad_dtype, head_dim;
+  hipStream_t st;
+};
+
+SA_HIDDEN int forward_bf16(const FwdCall& c);    // sa_bf16.hip
+SA_HIDDEN int backward_bf16(const BwdCall& c);
+SA_HIDDEN int forward_f32(const FwdCall& c);     // sa_f32.hip
+SA_HIDDEN int backward_f32(const BwdCall& c);
+
+}  // namespace sa_host

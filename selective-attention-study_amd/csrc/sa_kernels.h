@@ -4,22 +4,29 @@
 //   L_h = s Q_h K_h^T (causal),  S = relu(L_0) on E <= j < r,  F[i,j] = sum_{r<i} S[r,j],
 //   O_h = softmax(L_h - F) V_h.
 //
-// Kernels (all 256 threads = 4 wavefronts of 64; MFMA 32x32 tiles):
+// Kernels (all 256 threads = 4 wavefronts of 64; MFMA 32x32 tiles; the attention kernels order
+// their workgroups so that each XCD's L2 serves a contiguous range of heads):
 //   sel_colsum   head 0, one 32x32 (queries x keys) tile per step: column sums of S per
 //                32-query block -> colsum[b][rb][j]
 //   sel_scan     exclusive running sum of colsum over query blocks, seeded by the carried
 //                per-key state -> carry[b][rb][j], state_out[b][j]
 //   fwd          query-parallel. A wavefront owns 32 queries of G heads. Logit tiles are
 //                built transposed (keys x queries) so each lane holds one query: the online
-//                softmax row statistics stay in-lane; the selection's exclusive prefix over
-//                queries is a DPP lane scan, made once per tile and shared by the G heads.
-//                O^T = V^T P^T takes P straight from the accumulator registers.
-//   bwd          key-parallel. A wavefront owns 32 keys of G heads and sweeps the query
-//                tiles last to first. Tiles are (queries x keys), so the selection prefix F
-//                and the suffix U = sum_h sum_{i>r} dz_h[i,j] run down registers. dK, dV
-//                stay in registers; dQ goes through LDS and relaxed fp32 atomics. The head
-//                group holding head 0 folds g = -gate*U into head 0's own dz; other groups
-//                add their share of head 0's gradient with atomics.
+//                softmax row statistics stay in-lane, and O^T = V^T P^T takes P straight from
+//                the accumulator registers. Head 0's logits are built (queries x keys) instead,
+//                so the selection's prefix over queries runs down each lane's registers; F then
+//                reaches the softmax layout through the wavefront's LDS rows.
+//   bwd_kv       key-parallel. A wavefront owns 32 keys of G heads and sweeps the query tiles
+//                last to first. Tiles are (queries x keys), so the selection prefix F and the
+//                suffix U = sum_h sum_{i>r} dz_h[i,j] run down registers. dK, dV (and the
+//                group's share of head 0's dK) stay in registers; K, V rows sit in LDS. U is
+//                checkpointed per query tile for bwd_dq.
+//   bwd_dq       query-parallel. A wavefront owns 32 queries and walks the key tiles up to its
+//                diagonal, recomputing P, dz and the selection gradient g from the key side's
+//                U checkpoints; dQ = dz K takes dz through a per-wavefront LDS tile.
+//   bwd_finish   gradient epilogue: scale, add head 0's shares, convert to the output dtype.
+// The group holding head 0 folds g = -gate*U into head 0's own dz; other groups add their share
+// of head 0's gradients with atomics.
 //
 // MFMA operand layouts used throughout (v_mfma_f32_32x32x16_bf16 / v_mfma_f32_32x32x2_f32):
 //   C (32x32, 16 fp32 per lane): lane l holds column l%32, rows crow(i, l/32), i = 0..15,
@@ -29,26 +36,27 @@
 // A C-layout tile fed back as a B operand keeps its registers in place; the matching A operand
 // is then read with the C layout's row order (ld_perm).
 
+
+#pragma once
+
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 #include <math.h>
+
 #include <algorithm>
-#include <mutex>
 #include <type_traits>
 #include <utility>
-#include <vector>
 
-#include "sa.h"
+#include "sa_host.h"
 
 namespace {
+
+using namespace sa_host;
 
 typedef __bf16 bf16_t;
 typedef bf16_t bf16x8 __attribute__((__vector_size__(8 * sizeof(bf16_t))));
 typedef float f32x16 __attribute__((__vector_size__(16 * sizeof(float))));
 
-constexpr int TILE = 32;              // tile edge and carry checkpoint spacing (queries)
-constexpr int NTHREADS = 256;
-constexpr int NWAVES = 4;
 constexpr float LOG2E = 1.4426950408889634f;
 
 __device__ __forceinline__ int crow(int i, int h) { return 8 * (i >> 2) + 4 * h + (i & 3); }
@@ -587,8 +595,13 @@ __global__ __launch_bounds__(NTHREADS, (fwd_min_blocks<OP, D, G>())) void fwd_ke
     if (t + 1 < wg_end) load_tile(kt - 1);
     if (kt < my_end) {
       const int kbase = kt * TILE;
-      auto body = [&](auto edge_tag) {
-        constexpr bool EDGE = decltype(edge_tag)::value;
+      // edge: some key of the tile does not strictly precede every query of the block, lies past
+      // the end or is exempt; interior tiles skip the masks (the selection gate is then the logit's
+      // sign alone)
+      const bool edge = (kbase + TILE - 1 >= q_off + rb * TILE) || (kbase + TILE > Tk) || kbase < exempt;
+      // (one body for both kinds of tile: two copies of its accumulating products would make the
+      // compiler copy the output sums between register sets every tile)
+      auto body = [&]() {
         // Head 0's logits as (queries x keys), lane = key kbase + n: the selection's running sum
         // over queries then stays within the lane. F (log2 units) = the carry at the block's first
         // query + the selection by the block's earlier queries; it returns to the (keys x queries)
@@ -604,7 +617,7 @@ __global__ __launch_bounds__(NTHREADS, (fwd_min_blocks<OP, D, G>())) void fwd_ke
           f32x16 sel;
 #pragma unroll
           for (int i = 0; i < 16; ++i) sel[i] = fmaxf(l0t[i] * sl2, 0.f);
-          if constexpr (EDGE) {
+          if (edge) {
             // pairs exempt <= j < r; keys past the end and queries past the end hold zero rows
             const int jk = kbase + n;
             const int thr = jk >= exempt ? jk - (q_off + rb * TILE) - 4 * h : 32;
@@ -645,17 +658,16 @@ __global__ __launch_bounds__(NTHREADS, (fwd_min_blocks<OP, D, G>())) void fwd_ke
           f32x16 lg = zero16();
 #pragma unroll
           for (int s = 0; s < NS; ++s) lg = OP::mma(OP::ld_std(sK[buf][g], LDK, n, h, s), qf[g][s], lg);
+#pragma unroll
+          for (int i = 0; i < 16; ++i) lg[i] = fmaf(lg[i], sl2, -fs[i]);
+          if (edge) {   // keys j = kbase + crow(i, h) <= min(q_abs, Tk - 1)
+            const int thr = min(q_abs, Tk - 1) - kbase - 4 * h;
+#pragma unroll
+            for (int i = 0; i < 16; ++i) lg[i] = crow(i, 0) <= thr ? lg[i] : -INFINITY;
+          }
           float zmax = -INFINITY;
 #pragma unroll
-          for (int i = 0; i < 16; ++i) {
-            float z = fmaf(lg[i], sl2, -fs[i]);
-            if constexpr (EDGE) {
-              const int j = kbase + crow(i, h);
-              if (j > q_abs || j >= Tk) z = -INFINITY;
-            }
-            lg[i] = z;
-            zmax = fmaxf(zmax, z);
-          }
+          for (int i = 0; i < 16; ++i) zmax = fmaxf(zmax, lg[i]);
           const Halves zh = halves(zmax);
           const float m_new = fmaxf(m[g], fmaxf(zh.lo, zh.hi));
           if (__any(m_new > m[g])) {   // some row's maximum rose: rescale what was accumulated
@@ -686,11 +698,7 @@ __global__ __launch_bounds__(NTHREADS, (fwd_min_blocks<OP, D, G>())) void fwd_ke
               o[g][db] = OP::mma(OP::ld_perm(sVt[buf][g], LDV, db * 32 + n, h, s), pf[s], o[g][db]);
         }
       };
-      // interior: every key of the tile strictly precedes every query of the block (j < r, so the
-      // selection gate is the logit's sign alone) and lies inside the sequence
-      const bool edge = (kbase + TILE - 1 >= q_off + rb * TILE) || (kbase + TILE > Tk) || kbase < exempt;
-      if (edge) body(std::true_type{});
-      else body(std::false_type{});
+      body();
     }
     if constexpr (NBUF == 1) __syncthreads();   // the one buffer is free again
     if (t + 1 < wg_end) store_tile(NBUF == 2 ? buf ^ 1 : 0);
@@ -1025,10 +1033,10 @@ __global__ __launch_bounds__(NTHREADS, (kv_min_blocks<OP, D, G>())) void bwd_kv_
     if constexpr (KVLDS) return kv_lds(2 * g + 1, s);
     else return vf[g][s];
   };
-  // head 0's K: the group's own when it holds head 0
-  auto k0_frag = [&](int s) -> frag {
-    if constexpr (KVLDS) return kv_lds(has_h0 ? 0 : 2 * G, s);
-    else return has_h0 ? kf[0][s] : k0f[s];
+  // head 0's K: the group's own when it holds head 0 (h0)
+  auto k0_frag = [&](bool h0, int s) -> frag {
+    if constexpr (KVLDS) return kv_lds(h0 ? 0 : 2 * G, s);
+    else return h0 ? kf[0][s] : k0f[s];
   };
 
   f32x16 dkt[G][DB], dvt[G][DB], dk0t[DB];
@@ -1116,96 +1124,104 @@ __global__ __launch_bounds__(NTHREADS, (kv_min_blocks<OP, D, G>())) void bwd_kv_
   // their dV / dK sums run over all of them: their products take the split operands.
   const bool split_keys = key0 < exempt;
 
-  float hist_next = 0.f;
-  if constexpr (KV_PIPE) {
-    load_tile(NB - 1);
-    hist_next = carry_col[(int64_t)(NB - 1) * T];
-    store_tile(0);
-    __syncthreads();
-  }
-
-  for (int t = 0; t < ntiles; ++t) {
-    const int qb = NB - 1 - t;
-    const int qbase = qb * TILE;
-    const int buf = NBUF == 2 ? (t & 1) : 0;
-    float hist;
+  // The tile loop in two instances, for the group holding head 0 and for the others: one loop
+  // with a run-time choice between their accumulations makes the compiler copy the sums between
+  // register sets every tile.
+  auto sweep = [&](auto h0_tag) {
+    constexpr bool H0 = decltype(h0_tag)::value;
+    float hist_next = 0.f;
     if constexpr (KV_PIPE) {
-      hist = hist_next;
-      if (t + 1 < ntiles) {
-        load_tile(qb - 1);
-        hist_next = carry_col[(int64_t)(qb - 1) * T];
-      }
-    } else {
-      load_tile(qb);
-      hist = carry_col[(int64_t)qb * T];
-      if (t > 0) __syncthreads();   // every wavefront is done with the previous tile
+      load_tile(NB - 1);
+      hist_next = carry_col[(int64_t)(NB - 1) * T];
       store_tile(0);
       __syncthreads();
     }
-    if (qbase + TILE - 1 >= key0) {   // else every query of the tile precedes every key
-      if (h == 0 && j < T) uplane[(int64_t)qb * T + j] = ucarry;
-      // tile body; edge: some pair of the tile is masked (diagonal, sequence end) or exempt
-      // (rows past the end and keys past the end need no mask on the key side: the latter's sums
-      // stay in their own lanes, which are never written)
-      const bool edge = (qbase <= key0 + TILE - 1) || key0 < exempt;
-      const TileMasks mk(j, qbase, T, exempt, h);
-      // (a lambda: inlined late, its loop-invariant parts are not hoisted out of the tile loop,
-      // which would hold them in registers across it)
-      auto body = [&]() {
-        const elem* q0s = has_h0 ? sQ[buf][0] : sQ[buf][G];
-        f32x16 l0 = zero16();
-#pragma unroll
-        for (int s = 0; s < NS; ++s) l0 = OP::mma(OP::ld_std(q0s, LDK, n, h, s), k0_frag(s), l0);
-        f32x16 fs;
-        uint32_t gate;
-        selection_tile<true>(l0, (j < T) ? hist * LOG2E : 0.f, sl2, h, edge, mk, gate, fs);
 
-        // Per head: P and dz, dV^T += dO^T P, dK^T += Q^T dz; then g from the group's dz sum goes to
-        // head 0's dK: added to head 0's own dz when the group holds it, else into dk0t.
-        f32x16 dzsum, dz0;
-#pragma unroll
-        for (int g = 0; g < G; ++g) {
-          f32x16 lg;
-          if (has_h0 && g == 0) {   // head 0 itself: its logits are l0
-            lg = l0;
-          } else {
-            lg = zero16();
-#pragma unroll
-            for (int s = 0; s < NS; ++s) lg = OP::mma(OP::ld_std(sQ[buf][g], LDK, n, h, s), k_frag(g, s), lg);
-          }
-          f32x16 dp = zero16();
-#pragma unroll
-          for (int s = 0; s < NS; ++s) dp = OP::mma(OP::ld_std(sdO[buf][g], LDK, n, h, s), v_frag(g, s), dp);
-          f32x16 pr, dz;
-          p_dz_tile<true>(lg, dp, fs, sLse[buf][g], sDb[buf][g], sl2, h, edge, mk, pr, dz);
-          acc_t(dvt[g], sdOt[buf][g], pr, split_keys);
-          if (g == 0) {
-            dzsum = dz;
-          } else {
-#pragma unroll
-            for (int i = 0; i < 16; ++i) dzsum[i] += dz[i];
-          }
-          if (has_h0 && g == 0) dz0 = dz;   // head 0's dK waits for g
-          else acc_t(dkt[g], sQt[buf][g], dz, split_keys);
+    for (int t = 0; t < ntiles; ++t) {
+      const int qb = NB - 1 - t;
+      const int qbase = qb * TILE;
+      const int buf = NBUF == 2 ? (t & 1) : 0;
+      float hist;
+      if constexpr (KV_PIPE) {
+        hist = hist_next;
+        if (t + 1 < ntiles) {
+          load_tile(qb - 1);
+          hist_next = carry_col[(int64_t)(qb - 1) * T];
         }
-        f32x16 gp;
-        ucarry = gpath_tile(dzsum, ucarry, gate, h, gp);
-        if (has_h0) {
-#pragma unroll
-          for (int i = 0; i < 16; ++i) dz0[i] += gp[i];
-          acc_t(dkt[0], sQt[buf][0], dz0, true);
-        } else {
-          acc_t(dk0t, sQt[buf][G], gp, big_tile(gp));
-        }
-      };
-      body();
+      } else {
+        load_tile(qb);
+        hist = carry_col[(int64_t)qb * T];
+        if (t > 0) __syncthreads();   // every wavefront is done with the previous tile
+        store_tile(0);
+        __syncthreads();
+      }
+      if (qbase + TILE - 1 >= key0) {   // else every query of the tile precedes every key
+        if (h == 0 && j < T) uplane[(int64_t)qb * T + j] = ucarry;
+        // tile body; edge: some pair of the tile is masked (diagonal, sequence end) or exempt
+        // (rows past the end and keys past the end need no mask on the key side: the latter's sums
+        // stay in their own lanes, which are never written)
+        const bool edge = (qbase <= key0 + TILE - 1) || key0 < exempt;
+        const TileMasks mk(j, qbase, T, exempt, h);
+        // (a lambda: inlined late, its loop-invariant parts are not hoisted out of the tile loop,
+        // which would hold them in registers across it)
+        auto body = [&]() {
+          const elem* q0s = H0 ? sQ[buf][0] : sQ[buf][G];
+          f32x16 l0 = zero16();
+  #pragma unroll
+          for (int s = 0; s < NS; ++s) l0 = OP::mma(OP::ld_std(q0s, LDK, n, h, s), k0_frag(H0, s), l0);
+          f32x16 fs;
+          uint32_t gate;
+          selection_tile<true>(l0, (j < T) ? hist * LOG2E : 0.f, sl2, h, edge, mk, gate, fs);
+
+          // Per head: P and dz, dV^T += dO^T P, dK^T += Q^T dz; then g from the group's dz sum goes to
+          // head 0's dK: added to head 0's own dz when the group holds it, else into dk0t.
+          f32x16 dzsum, dz0;
+  #pragma unroll
+          for (int g = 0; g < G; ++g) {
+            f32x16 lg;
+            if (H0 && g == 0) {   // head 0 itself: its logits are l0
+              lg = l0;
+            } else {
+              lg = zero16();
+  #pragma unroll
+              for (int s = 0; s < NS; ++s) lg = OP::mma(OP::ld_std(sQ[buf][g], LDK, n, h, s), k_frag(g, s), lg);
+            }
+            f32x16 dp = zero16();
+  #pragma unroll
+            for (int s = 0; s < NS; ++s) dp = OP::mma(OP::ld_std(sdO[buf][g], LDK, n, h, s), v_frag(g, s), dp);
+            f32x16 pr, dz;
+            p_dz_tile<true>(lg, dp, fs, sLse[buf][g], sDb[buf][g], sl2, h, edge, mk, pr, dz);
+            acc_t(dvt[g], sdOt[buf][g], pr, split_keys);
+            if (g == 0) {
+              dzsum = dz;
+            } else {
+  #pragma unroll
+              for (int i = 0; i < 16; ++i) dzsum[i] += dz[i];
+            }
+            if (H0 && g == 0) dz0 = dz;   // head 0's dK waits for g
+            else acc_t(dkt[g], sQt[buf][g], dz, split_keys);
+          }
+          f32x16 gp;
+          ucarry = gpath_tile(dzsum, ucarry, gate, h, gp);
+          if constexpr (H0) {
+  #pragma unroll
+            for (int i = 0; i < 16; ++i) dz0[i] += gp[i];
+            acc_t(dkt[0], sQt[buf][0], dz0, true);
+          } else {
+            acc_t(dk0t, sQt[buf][G], gp, big_tile(gp));
+          }
+        };
+        body();
+      }
+      if constexpr (KV_PIPE) {
+        if constexpr (NBUF == 1) __syncthreads();   // the one buffer is free again
+        if (t + 1 < ntiles) store_tile(NBUF == 2 ? buf ^ 1 : 0);
+        __syncthreads();
+      }
     }
-    if constexpr (KV_PIPE) {
-      if constexpr (NBUF == 1) __syncthreads();   // the one buffer is free again
-      if (t + 1 < ntiles) store_tile(NBUF == 2 ? buf ^ 1 : 0);
-      __syncthreads();
-    }
-  }
+  };
+  if (has_h0) sweep(std::true_type{});
+  else sweep(std::false_type{});
 
   if (j >= T) return;
 #pragma unroll
@@ -1427,96 +1443,103 @@ __global__ __launch_bounds__(NTHREADS, (dq_min_blocks<OP, D>())) void bwd_dq_ker
     uv = (jj < T) ? urow[jj] : 0.f;
   };
 
-  float hist_next = 0.f, u_next = 0.f;
-  if constexpr (DQ_PIPE) {
-    load_tile(0);
-    key_vals(0, hist_next, u_next);
-    store_tile(0);
-    __syncthreads();
-  }
-
-  for (int ktile = 0; ktile < wg_end; ++ktile) {
-    const int kbase = ktile * TILE;
-    const int buf = NBUF == 2 ? (ktile & 1) : 0;
-    float hist, uin;
+  // The tile loop in two instances, for the group holding head 0 and for the others (as on the
+  // key side).
+  auto sweep = [&](auto h0_tag) {
+    constexpr bool H0 = decltype(h0_tag)::value;
+    float hist_next = 0.f, u_next = 0.f;
     if constexpr (DQ_PIPE) {
-      hist = hist_next;
-      uin = u_next;
-      if (ktile + 1 < wg_end) {
-        load_tile(ktile + 1);
-        key_vals(ktile + 1, hist_next, u_next);
-      }
-    } else {
-      load_tile(ktile);
-      key_vals(ktile, hist, uin);
-      if (ktile > 0) __syncthreads();   // every wavefront is done with the previous tile
+      load_tile(0);
+      key_vals(0, hist_next, u_next);
       store_tile(0);
       __syncthreads();
     }
-    if (ktile < my_end) {
-      const int j = kbase + n;
-      // tile body; edge: some pair of the tile is masked (diagonal, sequence end) or exempt
-      const bool edge = (kbase + TILE - 1 >= qbase) || (kbase + TILE > T) || kbase < exempt;
-      const TileMasks mk(j, qbase, T, exempt, h);
-      {
-        const elem* k0s = has_h0 ? sK[buf][0] : sK[buf][G];
-        f32x16 l0 = zero16();
-#pragma unroll
-        for (int s = 0; s < NS; ++s)
-          l0 = OP::mma(has_h0 ? q_frag(0, s) : q0a[s], OP::ld_std(k0s, LDK, n, h, s), l0);
-        f32x16 fs;
-        uint32_t gate;
-        selection_tile<false>(l0, hist * LOG2E, sl2, h, edge, mk, gate, fs);
 
-        f32x16 zsum, dz0;
-#pragma unroll
-        for (int g = 0; g < G; ++g) {
-          f32x16 lg;
-          if (has_h0 && g == 0) {   // head 0 itself: its logits are l0, its dQ waits for g
-            lg = l0;
-          } else {
-            lg = zero16();
-#pragma unroll
-            for (int s = 0; s < NS; ++s)
-              lg = OP::mma(q_frag(g, s), OP::ld_std(sK[buf][g], LDK, n, h, s), lg);
-          }
-          f32x16 dp = zero16();
-#pragma unroll
-          for (int s = 0; s < NS; ++s)
-            dp = OP::mma(do_frag(g, s), OP::ld_std(sV[buf][g], LDK, n, h, s), dp);
-          f32x16 pr, dz;
-          p_dz_tile<false>(lg, dp, fs, sLse[wave][g], sDb[wave][g], sl2, h, edge, mk, pr, dz);
-          if (g == 0) {
-            zsum = dz;
-          } else {
-#pragma unroll
-            for (int i = 0; i < 16; ++i) zsum[i] += dz[i];
-          }
-          if (has_h0 && g == 0) {
-            dz0 = dz;
-          } else {
-            acc_xk(dqacc[g], dz, sKt[buf][g], false);
-          }
+    for (int ktile = 0; ktile < wg_end; ++ktile) {
+      const int kbase = ktile * TILE;
+      const int buf = NBUF == 2 ? (ktile & 1) : 0;
+      float hist, uin;
+      if constexpr (DQ_PIPE) {
+        hist = hist_next;
+        uin = u_next;
+        if (ktile + 1 < wg_end) {
+          load_tile(ktile + 1);
+          key_vals(ktile + 1, hist_next, u_next);
         }
+      } else {
+        load_tile(ktile);
+        key_vals(ktile, hist, uin);
+        if (ktile > 0) __syncthreads();   // every wavefront is done with the previous tile
+        store_tile(0);
+        __syncthreads();
+      }
+      if (ktile < my_end) {
+        const int j = kbase + n;
+        // tile body; edge: some pair of the tile is masked (diagonal, sequence end) or exempt
+        const bool edge = (kbase + TILE - 1 >= qbase) || (kbase + TILE > T) || kbase < exempt;
+        const TileMasks mk(j, qbase, T, exempt, h);
+        {
+          const elem* k0s = H0 ? sK[buf][0] : sK[buf][G];
+          f32x16 l0 = zero16();
+  #pragma unroll
+          for (int s = 0; s < NS; ++s)
+            l0 = OP::mma(H0 ? q_frag(0, s) : q0a[s], OP::ld_std(k0s, LDK, n, h, s), l0);
+          f32x16 fs;
+          uint32_t gate;
+          selection_tile<false>(l0, hist * LOG2E, sl2, h, edge, mk, gate, fs);
 
-        f32x16 gp;
-        gpath_tile(zsum, uin, gate, h, gp);
-        if (has_h0) {
-          f32x16 dzh;
-#pragma unroll
-          for (int i = 0; i < 16; ++i) dzh[i] = dz0[i] + gp[i];
-          acc_xk(dqacc[0], dzh, sKt[buf][0], true);
-        } else {
-          acc_xk(dq0acc, gp, sKt[buf][G], big_tile(gp));
+          f32x16 zsum, dz0;
+  #pragma unroll
+          for (int g = 0; g < G; ++g) {
+            f32x16 lg;
+            if (H0 && g == 0) {   // head 0 itself: its logits are l0, its dQ waits for g
+              lg = l0;
+            } else {
+              lg = zero16();
+  #pragma unroll
+              for (int s = 0; s < NS; ++s)
+                lg = OP::mma(q_frag(g, s), OP::ld_std(sK[buf][g], LDK, n, h, s), lg);
+            }
+            f32x16 dp = zero16();
+  #pragma unroll
+            for (int s = 0; s < NS; ++s)
+              dp = OP::mma(do_frag(g, s), OP::ld_std(sV[buf][g], LDK, n, h, s), dp);
+            f32x16 pr, dz;
+            p_dz_tile<false>(lg, dp, fs, sLse[wave][g], sDb[wave][g], sl2, h, edge, mk, pr, dz);
+            if (g == 0) {
+              zsum = dz;
+            } else {
+  #pragma unroll
+              for (int i = 0; i < 16; ++i) zsum[i] += dz[i];
+            }
+            if (H0 && g == 0) {
+              dz0 = dz;
+            } else {
+              acc_xk(dqacc[g], dz, sKt[buf][g], false);
+            }
+          }
+
+          f32x16 gp;
+          gpath_tile(zsum, uin, gate, h, gp);
+          if constexpr (H0) {
+            f32x16 dzh;
+  #pragma unroll
+            for (int i = 0; i < 16; ++i) dzh[i] = dz0[i] + gp[i];
+            acc_xk(dqacc[0], dzh, sKt[buf][0], true);
+          } else {
+            acc_xk(dq0acc, gp, sKt[buf][G], big_tile(gp));
+          }
         }
       }
+      if constexpr (DQ_PIPE) {
+        if constexpr (NBUF == 1) __syncthreads();   // the one buffer is free again
+        if (ktile + 1 < wg_end) store_tile(NBUF == 2 ? buf ^ 1 : 0);
+        __syncthreads();
+      }
     }
-    if constexpr (DQ_PIPE) {
-      if constexpr (NBUF == 1) __syncthreads();   // the one buffer is free again
-      if (ktile + 1 < wg_end) store_tile(NBUF == 2 ? buf ^ 1 : 0);
-      __syncthreads();
-    }
-  }
+  };
+  if (has_h0) sweep(std::true_type{});
+  else sweep(std::false_type{});
 
   if (qb >= NB) return;
 #pragma unroll
@@ -1567,71 +1590,9 @@ __global__ __launch_bounds__(NTHREADS) void bwd_finish_kernel(
   }
 }
 
+
 // ---------------------------------------------------------------------------------------------
-// Host side.
-
-// Event timing of the main kernels, for measurement tools (sa_timing_enable / sa_timing_read).
-// Off by default; when on, each timed launch is bracketed by a pair of HIP events recorded on the
-// launch's own stream. The registry is the only mutable host state of the library.
-struct TimingRegistry {
-  std::mutex mu;
-  bool on = false;
-  std::vector<std::pair<hipEvent_t, hipEvent_t>> events[SA_KERNEL_COUNT];
-};
-TimingRegistry& timing() {
-  static TimingRegistry r;
-  return r;
-}
-
-// Brackets one launch: construct before it, destroy after it (both on stream st).
-class TimedLaunch {
- public:
-  TimedLaunch(int kernel, hipStream_t st) : kernel_(kernel), st_(st) {
-    TimingRegistry& r = timing();
-    std::lock_guard<std::mutex> lock(r.mu);
-    if (!r.on) return;
-    if (hipEventCreate(&start_) != hipSuccess) return;
-    if (hipEventCreate(&stop_) != hipSuccess) {
-      (void)hipEventDestroy(start_);
-      return;
-    }
-    active_ = hipEventRecord(start_, st_) == hipSuccess;
-  }
-  ~TimedLaunch() {
-    if (!active_) return;
-    TimingRegistry& r = timing();
-    std::lock_guard<std::mutex> lock(r.mu);
-    if (hipEventRecord(stop_, st_) == hipSuccess) r.events[kernel_].emplace_back(start_, stop_);
-  }
-
- private:
-  int kernel_;
-  hipStream_t st_;
-  hipEvent_t start_ = nullptr, stop_ = nullptr;
-  bool active_ = false;
-};
-
-inline int64_t align_up(int64_t x, int64_t a) { return (x + a - 1) / a * a; }
-inline int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
-
-inline int launch_status() { return hipGetLastError() == hipSuccess ? SA_OK : SA_ERR_LAUNCH; }
-
-#ifndef SA_FWD_GROUP_D64
-#define SA_FWD_GROUP_D64 1
-#endif
-int auto_group(int dtype, int64_t D, int64_t heads, int requested, bool backward) {
-  int g = requested;
-  if (g <= 0) {
-    if (dtype == SA_DTYPE_F32) g = 1;
-    else if (backward) g = (D <= 32) ? 2 : 1;
-    else g = (D <= 32) ? 4 : (D <= 64 ? SA_FWD_GROUP_D64 : 1);
-  }
-  int cap = (dtype == SA_DTYPE_F32) ? 1 : (backward ? 2 : 4);
-  if (D >= 128 || (backward && D >= 64)) cap = 1;
-  g = g > cap ? cap : g;
-  while (g > 1 && (heads % g != 0)) g >>= 1;
-  return g < 1 ? 1 : g;
-}
+// Host side: launch sequences of one storage dtype and head dim.
 
 template <class OP, int D>
 int run_selection(const typename OP::elem* q, const typename OP::elem* k, float* carry, const float* state_in,
@@ -1692,45 +1653,6 @@ int forward_impl(const void* q_, const void* k_, const void* v_, float* out, flo
                          train_len, st);
   }
   return launch_status();
-}
-
-// Heads per wavefront of the backward kernels: a group shares head 0's selection work (its logits,
-// the history F and the g products), so wider groups amortise it, within the register budget.
-#ifndef SA_BWD_GROUP_DEFAULT
-#define SA_BWD_GROUP_DEFAULT 1
-#endif
-int bwd_group(int dtype, int64_t D, int64_t heads, int requested) {
-  int g = requested > 0 ? requested : SA_BWD_GROUP_DEFAULT;
-  const int cap = (dtype == SA_DTYPE_BF16 && D <= 32) ? 2 : 1;
-  g = g > cap ? cap : g;
-  while (g > 1 && (heads % g != 0)) g >>= 1;
-  return g < 1 ? 1 : g;
-}
-
-struct BwdLayout {
-  int64_t qt, dot, kt, lse, dbar, dq, dk, dv, dq0x, dk0x, ucheck, total;
-};
-
-// Workspace of sa_backward: transposed Q, dO, K; row statistics; fp32 gradient sums; head 0's
-// shares from other groups; the selection-suffix checkpoints (one plane per head group).
-BwdLayout bwd_layout(int64_t nseq, int64_t heads, int64_t t, int64_t D, int64_t esize, int64_t G) {
-  const int64_t R = nseq * heads, ldt = sa_transposed_ld(t), NB = (t + TILE - 1) / TILE;
-  BwdLayout L;
-  int64_t off = 0;
-  auto take = [&](int64_t bytes) { int64_t o = off; off = align_up(off + bytes, 256); return o; };
-  L.qt = take(R * D * ldt * esize);
-  L.dot = take(R * D * ldt * esize);
-  L.kt = take(R * D * ldt * esize);
-  L.lse = take(R * t * 4);
-  L.dbar = take(R * t * 4);
-  L.dq = take(R * t * D * 4);
-  L.dk = take(R * t * D * 4);
-  L.dv = take(R * t * D * 4);
-  L.dq0x = take(nseq * t * D * 4);
-  L.dk0x = take(nseq * t * D * 4);
-  L.ucheck = take((heads / G) * nseq * NB * t * 4);
-  L.total = off;
-  return L;
 }
 
 template <class OP, int D, int G>
@@ -1813,137 +1735,27 @@ int backward_impl(const void* q_, const void* k_, const void* v_, const float* o
   return launch_status();
 }
 
-bool valid_dims(int64_t nseq, int64_t heads, int64_t t) {
-  const int64_t lim = (int64_t)1 << 30;
-  return nseq >= 1 && heads >= 1 && t >= 1 && nseq < 65536 && heads < 65536 && t < lim && nseq * heads < 65536;
-}
-
-}  // namespace
-
-// ---------------------------------------------------------------------------------------------
-// C ABI
-
-extern "C" {
-
-int sa_abi_version(void) { return 2; }
-
-int sa_timing_enable(int on) {
-  TimingRegistry& r = timing();
-  std::lock_guard<std::mutex> lock(r.mu);
-  for (auto& list : r.events) {
-    for (auto& ev : list) {
-      (void)hipEventDestroy(ev.first);
-      (void)hipEventDestroy(ev.second);
-    }
-    list.clear();
-  }
-  r.on = on != 0;
-  return SA_OK;
-}
-
-int sa_timing_read(int kernel, double* total_ms, int64_t* launches) {
-  if (kernel < 0 || kernel >= SA_KERNEL_COUNT || !total_ms || !launches) return SA_ERR_ARGUMENT;
-  TimingRegistry& r = timing();
-  std::lock_guard<std::mutex> lock(r.mu);
-  double sum = 0.0;
-  for (auto& ev : r.events[kernel]) {
-    float ms = 0.f;
-    if (hipEventSynchronize(ev.second) != hipSuccess || hipEventElapsedTime(&ms, ev.first, ev.second) != hipSuccess)
-      return SA_ERR_LAUNCH;
-    sum += ms;
-  }
-  *total_ms = sum;
-  *launches = (int64_t)r.events[kernel].size();
-  return SA_OK;
-}
-
-const char* sa_status_string(int status) {
-  switch (status) {
-    case SA_OK: return "ok";
-    case SA_ERR_ARGUMENT: return "invalid argument (size, pointer or option)";
-    case SA_ERR_HEAD_DIM: return "head_dim must be 32, 64 or 128 at the C ABI";
-    case SA_ERR_DTYPE: return "unknown dtype code";
-    case SA_ERR_WORKSPACE: return "workspace too small";
-    case SA_ERR_LAUNCH: return "HIP kernel launch failed";
-    default: return "unknown status";
-  }
-}
-
-int64_t sa_transposed_ld(int64_t t) { return align_up(t < 1 ? 1 : t, 64); }
-
-int64_t sa_forward_workspace_bytes(int64_t nseq, int64_t heads, int64_t tk, int64_t head_dim, int dtype) {
-  const int64_t es = dtype == SA_DTYPE_BF16 ? 2 : 4;
-  return align_up(nseq * heads * head_dim * sa_transposed_ld(tk) * es, 256);
-}
-
-int sa_forward(const void* q, const void* k, const void* v, float* out, float* rmax, float* rden, float* carry,
-               const float* state_in, float* state_out, int64_t state_ld, void* workspace,
-               int64_t workspace_bytes, int64_t nseq, int64_t heads, int64_t tq, int64_t tk, int64_t q_offset,
-               int64_t kv_stride, int64_t head_dim, float scale, int dtype, int exempt, int group, int damp_mode,
-               int64_t train_len, void* stream) {
-  if (!valid_dims(nseq, heads, tk) || tq < 1 || q_offset < 0 || q_offset + tq != tk) return SA_ERR_ARGUMENT;
-  if (kv_stride == 0) kv_stride = tk * head_dim;
-  if (kv_stride < tk * head_dim || kv_stride % 8 != 0) return SA_ERR_ARGUMENT;
-  if (!q || !k || !v || !out || !rmax || !rden || !carry || !state_out || !workspace) return SA_ERR_ARGUMENT;
-  if (q_offset > 0 && !state_in) return SA_ERR_ARGUMENT;
-  if (state_ld < tk || exempt < 1 || damp_mode < 0 || damp_mode > 2 || (damp_mode && train_len < 1))
-    return SA_ERR_ARGUMENT;
-  if (!(scale > 0.f) || !(scale < INFINITY)) return SA_ERR_ARGUMENT;
-  if (dtype != SA_DTYPE_BF16 && dtype != SA_DTYPE_F32) return SA_ERR_DTYPE;
-  if (head_dim != 32 && head_dim != 64 && head_dim != 128) return SA_ERR_HEAD_DIM;
-  if (workspace_bytes < sa_forward_workspace_bytes(nseq, heads, tk, head_dim, dtype)) return SA_ERR_WORKSPACE;
-  hipStream_t st = static_cast<hipStream_t>(stream);
-  const int ns = (int)nseq, H = (int)heads, Tq = (int)tq, Tk = (int)tk, qo = (int)q_offset;
-  const float tl = (float)train_len;
-#define SA_FWD(OPT, DD)                                                                                             \
-  return forward_impl<OPT, DD>(q, k, v, out, rmax, rden, carry, state_in, state_out, state_ld, workspace, ns, H, Tq, \
-                               Tk, kv_stride, qo, scale, exempt, group, damp_mode, tl, st)
-  if (dtype == SA_DTYPE_BF16) {
-    if (head_dim == 32) SA_FWD(OpBF16, 32);
-    if (head_dim == 64) SA_FWD(OpBF16, 64);
-    SA_FWD(OpBF16, 128);
-  } else {
-    if (head_dim == 32) SA_FWD(OpF32, 32);
-    if (head_dim == 64) SA_FWD(OpF32, 64);
-    SA_FWD(OpF32, 128);
-  }
+template <class OP>
+int forward_entry(const FwdCall& c) {
+#define SA_FWD(DD)                                                                                                 \
+  return forward_impl<OP, DD>(c.q, c.k, c.v, c.out, c.rmax, c.rden, c.carry, c.state_in, c.state_out, c.state_ld, \
+                              c.ws, c.nseq, c.H, c.Tq, c.Tk, c.kvs, c.q_off, c.scale, c.exempt, c.group,           \
+                              c.damp_mode, c.train_len, c.st)
+  if (c.head_dim == 32) SA_FWD(32);
+  if (c.head_dim == 64) SA_FWD(64);
+  SA_FWD(128);
 #undef SA_FWD
 }
 
-int64_t sa_backward_workspace_bytes(int64_t nseq, int64_t heads, int64_t t, int64_t head_dim, int dtype, int group) {
-  if (!valid_dims(nseq, heads, t) || (dtype != SA_DTYPE_BF16 && dtype != SA_DTYPE_F32)) return -1;
-  return bwd_layout(nseq, heads, t, head_dim, dtype == SA_DTYPE_BF16 ? 2 : 4, bwd_group(dtype, head_dim, heads, group))
-      .total;
-}
-
-int sa_backward(const void* q, const void* k, const void* v, const float* out, const void* dout, const float* rmax,
-                const float* rden, const float* carry, void* dq, void* dk, void* dv, void* workspace,
-                int64_t workspace_bytes, int64_t nseq, int64_t heads, int64_t t, int64_t head_dim, float scale,
-                int dtype, int grad_dtype, int exempt, int group, void* stream) {
-  if (!valid_dims(nseq, heads, t) || exempt < 1) return SA_ERR_ARGUMENT;
-  if (!(scale > 0.f) || !(scale < INFINITY)) return SA_ERR_ARGUMENT;
-  if (!q || !k || !v || !out || !dout || !rmax || !rden || !carry || !dq || !dk || !dv || !workspace)
-    return SA_ERR_ARGUMENT;
-  if (dtype != SA_DTYPE_BF16 && dtype != SA_DTYPE_F32) return SA_ERR_DTYPE;
-  if (grad_dtype != SA_DTYPE_BF16 && grad_dtype != SA_DTYPE_F32) return SA_ERR_DTYPE;
-  if (head_dim != 32 && head_dim != 64 && head_dim != 128) return SA_ERR_HEAD_DIM;
-  if (group < 0 || workspace_bytes < sa_backward_workspace_bytes(nseq, heads, t, head_dim, dtype, group))
-    return SA_ERR_WORKSPACE;
-  hipStream_t st = static_cast<hipStream_t>(stream);
-  const int ns = (int)nseq, H = (int)heads, T = (int)t;
-#define SA_BWD(OPT, DD) \
-  return backward_impl<OPT, DD>(q, k, v, out, dout, rmax, rden, carry, dq, dk, dv, workspace, ns, H, T, scale, exempt, \
-                                group, grad_dtype, st)
-  if (dtype == SA_DTYPE_BF16) {
-    if (head_dim == 32) SA_BWD(OpBF16, 32);
-    if (head_dim == 64) SA_BWD(OpBF16, 64);
-    SA_BWD(OpBF16, 128);
-  } else {
-    if (head_dim == 32) SA_BWD(OpF32, 32);
-    if (head_dim == 64) SA_BWD(OpF32, 64);
-    SA_BWD(OpF32, 128);
-  }
+template <class OP>
+int backward_entry(const BwdCall& c) {
+#define SA_BWD(DD)                                                                                                 \
+  return backward_impl<OP, DD>(c.q, c.k, c.v, c.out, c.dout, c.rmax, c.rden, c.carry, c.dq, c.dk, c.dv, c.ws,    \
+                               c.nseq, c.H, c.T, c.scale, c.exempt, c.group, c.grad_dtype, c.st)
+  if (c.head_dim == 32) SA_BWD(32);
+  if (c.head_dim == 64) SA_BWD(64);
+  SA_BWD(128);
 #undef SA_BWD
 }
 
-}  // extern "C"
+}  // namespace
