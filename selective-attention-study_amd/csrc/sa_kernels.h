@@ -455,7 +455,19 @@ __global__ __launch_bounds__(NTHREADS) void sel_scan_kernel(
   if (j >= Tk) return;
   float run = (state_in != nullptr && j < q_off) ? state_in[(int64_t)b * state_ld + j] : 0.f;
   float* col = carry + (int64_t)b * NBq * Tk + j;
-  for (int rb = 0; rb < NBq; ++rb) {
+  constexpr int U = 16;   // blocks per step: their loads are issued together
+  int rb = 0;
+  for (; rb + U <= NBq; rb += U) {
+    float c[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) c[u] = col[(int64_t)(rb + u) * Tk];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      col[(int64_t)(rb + u) * Tk] = run;
+      run += c[u];
+    }
+  }
+  for (; rb < NBq; ++rb) {
     const float c = col[(int64_t)rb * Tk];
     col[(int64_t)rb * Tk] = run;
     run += c;
@@ -731,41 +743,72 @@ __global__ __launch_bounds__(NTHREADS, (fwd_min_blocks<OP, D, G>())) void fwd_ke
 
 // ---------------------------------------------------------------------------------------------
 // Backward preparation: lse = rmax + log2(rden), dbar = rowsum(dO * O), and the transposed
-// copies Q^T, dO^T (R, D, ldt). One thread per row for the statistics; transposes by tiles.
+// copies Q^T, dO^T, K^T (R, D, ldt). The statistics take D/8 lanes per row (8 elements each, so
+// the loads of a row are contiguous across its lanes); transposes go by tiles.
 
 template <class OP, int D>
 __global__ __launch_bounds__(NTHREADS) void bwd_rowstats_kernel(
     const typename OP::elem* __restrict__ dout, const float* __restrict__ out,
     const float* __restrict__ rmax, const float* __restrict__ rden,
     float* __restrict__ lse, float* __restrict__ dbar, int64_t rows) {
-  const int64_t r = (int64_t)blockIdx.x * NTHREADS + threadIdx.x;
-  if (r >= rows) return;
-  const typename OP::elem* dr = dout + r * D;
-  const float* orow = out + r * D;
+  using elem = typename OP::elem;
+  constexpr int LPR = D / 8;   // lanes per row
+  const int64_t g = (int64_t)blockIdx.x * NTHREADS + threadIdx.x;
+  const int64_t r = g / LPR;
+  const int part = (int)(g % LPR);
   float acc = 0.f;
-#pragma unroll 8
-  for (int d = 0; d < D; ++d) acc += OP::to_float(dr[d]) * orow[d];
-  dbar[r] = acc;
-  lse[r] = rmax[r] + __log2f(rden[r]);
+  if (r < rows) {
+    const elem* dr = dout + r * D + part * 8;
+    const float* orow = out + r * D + part * 8;
+    const float4 o0 = *reinterpret_cast<const float4*>(orow);
+    const float4 o1 = *reinterpret_cast<const float4*>(orow + 4);
+    const float ov[8] = {o0.x, o0.y, o0.z, o0.w, o1.x, o1.y, o1.z, o1.w};
+    elem dv[8];
+    if constexpr (sizeof(elem) == 2) {
+      *reinterpret_cast<uint4*>(dv) = *reinterpret_cast<const uint4*>(dr);
+    } else {
+      *reinterpret_cast<float4*>(dv) = *reinterpret_cast<const float4*>(dr);
+      *reinterpret_cast<float4*>(dv + 4) = *reinterpret_cast<const float4*>(dr + 4);
+    }
+#pragma unroll
+    for (int e = 0; e < 8; ++e) acc += OP::to_float(dv[e]) * ov[e];
+  }
+#pragma unroll
+  for (int o = LPR / 2; o > 0; o >>= 1) acc += __shfl_xor(acc, o);
+  if (r < rows && part == 0) {
+    dbar[r] = acc;
+    lse[r] = rmax[r] + __log2f(rden[r]);
+  }
 }
 
-// in (R, T, D) -> outT (R, D, ldt); a workgroup moves a [64 t][D] slab through LDS.
+// in (R, T, D) -> outT (R, D, ldt), zero past T; a workgroup moves a [64 t][D] slab through LDS in
+// 16-byte chunks: row chunks in, then 8 (bf16) or 4 (fp32) consecutive t of one d out.
 template <typename E, int D>
 __global__ __launch_bounds__(NTHREADS) void transpose_kernel(const E* __restrict__ in, E* __restrict__ outT,
                                                              int T, int64_t ldt, int64_t in_stride) {
-  __shared__ E tile[64][D + 1];
+  constexpr int EPC = 16 / (int)sizeof(E);
+  constexpr int LDS_LD = D + EPC;   // padded row: 16-byte aligned, rows on shifted banks
+  __shared__ __attribute__((aligned(16))) E tile[64 * LDS_LD];
   const int64_t r = blockIdx.y;
   const int t0 = blockIdx.x * 64;
   const E* src = in + r * in_stride;
-  for (int c = threadIdx.x; c < 64 * D; c += NTHREADS) {
-    const int tt = c / D, d = c % D;
-    tile[tt][d] = (t0 + tt < T) ? src[(int64_t)(t0 + tt) * D + d] : (E)0;
+  for (int c = threadIdx.x; c < 64 * D / EPC; c += NTHREADS) {
+    const int tt = c / (D / EPC), d0 = (c % (D / EPC)) * EPC;
+    uint4 v = make_uint4(0u, 0u, 0u, 0u);
+    if (t0 + tt < T) v = *reinterpret_cast<const uint4*>(src + (int64_t)(t0 + tt) * D + d0);
+    *reinterpret_cast<uint4*>(&tile[tt * LDS_LD + d0]) = v;
   }
   __syncthreads();
   E* dst = outT + r * D * ldt;
-  for (int c = threadIdx.x; c < 64 * D; c += NTHREADS) {
-    const int d = c / 64, tt = c % 64;
-    if (t0 + tt < ldt) dst[(int64_t)d * ldt + t0 + tt] = tile[tt][d];
+  for (int c = threadIdx.x; c < D * 64 / EPC; c += NTHREADS) {
+    const int d = c % D, tt0 = (c / D) * EPC;
+    union {
+      uint4 v;
+      E e[EPC];
+    } u;
+#pragma unroll
+    for (int e = 0; e < EPC; ++e) u.e[e] = tile[(tt0 + e) * LDS_LD + d];
+    if (t0 + tt0 < ldt) *reinterpret_cast<uint4*>(dst + (int64_t)d * ldt + t0 + tt0) = u.v;
   }
 }
 
@@ -1705,8 +1748,8 @@ int backward_impl(const void* q_, const void* k_, const void* v_, const float* o
   hipLaunchKernelGGL((transpose_kernel<elem, D>), gt, dim3(NTHREADS), 0, st, q, qt, T, ldt, (int64_t)T * D);
   hipLaunchKernelGGL((transpose_kernel<elem, D>), gt, dim3(NTHREADS), 0, st, dout, dot, T, ldt, (int64_t)T * D);
   hipLaunchKernelGGL((transpose_kernel<elem, D>), gt, dim3(NTHREADS), 0, st, k, kt, T, ldt, (int64_t)T * D);
-  hipLaunchKernelGGL((bwd_rowstats_kernel<OP, D>), dim3((unsigned)cdiv(R * T, NTHREADS)), dim3(NTHREADS), 0, st,
-                     dout, out, rmax, rden, lse, dbar, R * T);
+  hipLaunchKernelGGL((bwd_rowstats_kernel<OP, D>), dim3((unsigned)cdiv(R * T * (D / 8), NTHREADS)), dim3(NTHREADS),
+                     0, st, dout, out, rmax, rden, lse, dbar, R * T);
   // head 0's shares from the other groups are atomic targets (one add per element and group)
   hipLaunchKernelGGL(fill_zero_kernel, dim3(256), dim3(NTHREADS), 0, st, reinterpret_cast<float4*>(dq0x),
                      (int64_t)((int64_t)nseq * T * D / 4));
