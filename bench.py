@@ -39,6 +39,13 @@ STEP_FLOP = 7.0 * UNIT             # fwd 2 products + bwd 5 (FlashAttention conv
 # Products each timed kernel computes (recomputation included): the forward QK^T and PV; the
 # key-side backward QK^T, dO V^T, P^T dO, dz^T Q; the query-side backward QK^T, dO V^T, dz K.
 KERNEL_FLOP = {"forward": 2.0 * UNIT, "backward_kv": 4.0 * UNIT, "backward_dq": 3.0 * UNIT}
+# HBM bytes per launch of each kernel at this workload, measured with rocprofv3's FETCH_SIZE and
+# WRITE_SIZE counters (one pass each) and scaled by a 1 GiB copy's readings (FETCH x 2.0, WRITE x
+# 1.0): profiles/c2_attention_kernels_traffic.md. The counters need the profiler, so bench.py
+# reports the committed measurement; re-measure after a kernel change.
+MEASURED_TRAFFIC_BYTES = {"forward": (2.0 * 462_817 + 67_584) * 1024,
+                          "backward_kv": (2.0 * 601_531 + 639_545) * 1024,
+                          "backward_dq": (2.0 * 558_147 + 126_976) * 1024}
 
 
 def _cpu_model() -> str:
@@ -165,7 +172,8 @@ def main() -> int:
         "roofline": {"bound": "mfma",
                      "kernel": f"{dominant} ({KERNEL_FLOP[dominant] / UNIT:.0f}*B*H*D*T^2 FLOP per launch)",
                      "achieved": round(achieved, 2), "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
-                     "frac": round(achieved / PEAK_BF16_TFLOPS, 4), "traffic": None},
+                     "frac": round(achieved / PEAK_BF16_TFLOPS, 4),
+                     "traffic": MEASURED_TRAFFIC_BYTES[dominant], "traffic_unit": "bytes per launch (rocprofv3)"},
     }
     if not args.no_train:
         # the metric's "train tok/s": C3, the reference's 209M geometry (d768, 12 heads x 64, 24 layers)
