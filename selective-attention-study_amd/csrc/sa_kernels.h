@@ -865,7 +865,7 @@ struct TileMasks {
 
 // Head 0's selection on a tile of its raw logits l0, in log2 units: sel = relu(s log2e l0) where
 // exempt <= j < r < T, and the history F[r, j] = hist2 + sum of sel over the tile's earlier rows
-// (the running sum runs down the rows; the half-wavefronts exchange partial sums). gate[i] is
+// (the running sum runs down the rows; the half-wavefronts exchange partial sums). Bit i of gate is
 // sel[i] > 0, the gate of the gradient path. `edge` (wave-uniform) marks tiles where some pair
 // fails exempt <= j < r: the mask is applied there (every tile when ALWAYS, which costs a few
 // instructions per element but no branch).
