@@ -47,7 +47,7 @@ extern "C" {
 #define SA_ERR_WORKSPACE -4     /* workspace smaller than the *_workspace_bytes figure */
 #define SA_ERR_LAUNCH -5        /* a kernel launch failed (hipGetLastError) */
 
-/* ABI revision of this header; bumps when a signature changes. */
+/* ABI revision of this header; bumps when a signature changes or an entry point is added. */
 int sa_abi_version(void);
 
 /* Human-readable text for a status code (static storage). */
@@ -56,7 +56,7 @@ const char* sa_status_string(int status);
 /*
  * Kernel timing for measurement tools; no counterpart in the reference (which times whole calls
  * with perf_counter, scripts/bench_kernels.py:36-58). While enabled, sa_forward and sa_backward
- * record a pair of HIP events on their stream around each of their main kernels.
+ * record a pair of HIP events on their stream around each of their main kernels (sa_decode too).
  * sa_timing_enable(on) discards what was recorded and switches recording on (1) or off (0).
  * sa_timing_read waits for the recorded events of one kernel and returns the summed duration in
  * milliseconds and the number of launches. Not meant for production paths: the events cost a
@@ -66,7 +66,8 @@ const char* sa_status_string(int status);
 #define SA_KERNEL_BACKWARD 1    /* the key-parallel backward kernel (dK, dV) */
 #define SA_KERNEL_SELECTION 2   /* head 0's selection column sums + scan */
 #define SA_KERNEL_BACKWARD_DQ 3 /* the query-parallel backward kernel (dQ) */
-#define SA_KERNEL_COUNT 4
+#define SA_KERNEL_DECODE 4      /* the decode step's cache-reading kernel */
+#define SA_KERNEL_COUNT 5
 int sa_timing_enable(int on);
 int sa_timing_read(int kernel, double* total_ms, int64_t* launches);
 
@@ -124,6 +125,27 @@ int sa_backward(const void* q, const void* k, const void* v, const float* out, c
                 void* workspace, int64_t workspace_bytes,
                 int64_t nseq, int64_t heads, int64_t t, int64_t head_dim, float scale, int dtype,
                 int grad_dtype, int exempt, int group, void* stream);
+
+/* Bytes of scratch sa_decode needs (per-chunk partial softmax sums) for t cached keys. */
+int64_t sa_decode_workspace_bytes(int64_t nseq, int64_t heads, int64_t t, int64_t head_dim);
+
+/*
+ * One cached decode step; replaces the PyTorch step of the reference's attention slot
+ * (src/selective_attention/mixers.py:115-130, `SelectiveAttention.step_cache`). The newest query
+ * of every head (position t-1) attends over the t cached keys, its own included, with the carried
+ * selection subtracted from its logits; then the selector head of every group adds this query's
+ * own selection relu(s q.k_j) to the state, for exempt <= j < t-1:
+ *   q          (nseq*heads, D)             this step's queries (storage dtype)
+ *   k, v       (nseq*heads, ., D)          the caches, heads kv_stride elements apart; keys 0..t-1
+ *   out        (nseq*heads, D)             fp32
+ *   selected   (nseq*groups, state_ld)     fp32 per-key selection, read, then updated in place
+ *   groups     selector groups per sequence: 1 = head 0 selects for every head (the shared
+ *              variant), heads = every head selects for itself; heads % groups == 0
+ * Logits, softmax and sums are fp32 on the upcast operands, as the reference's step.
+ */
+int sa_decode(const void* q, const void* k, const void* v, float* out, float* selected, int64_t state_ld,
+              void* workspace, int64_t workspace_bytes, int64_t nseq, int64_t heads, int64_t groups, int64_t t,
+              int64_t kv_stride, int64_t head_dim, float scale, int dtype, int exempt, void* stream);
 
 #ifdef __cplusplus
 }

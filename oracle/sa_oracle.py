@@ -28,6 +28,8 @@ How each function is pinned (tests/test_oracle.py):
   tail                 == the last rows of `attention` (chunked summation of the history)
   prefill_chunks       == `attention` (chunk state carried between calls)
   decode_steps         == `attention` (one query at a time, reference mixers.py:115-130)
+  decode_step          through decode_steps (its every step); a step from an arbitrary state ==
+                          the softmax written out with exp and sums
   per_head             == every head run alone as a one-head sequence (mixers.py:76-84)
 No function here is "parity unpinned".
 """
@@ -176,20 +178,31 @@ def prefill_chunks(q, k, v, chunk: int, exempt: int = 1):
     return torch.cat(outs, dim=2), state
 
 
+def decode_step(q1, k, v, state, exempt: int = 1):
+    """One cached step (reference mixers.py:115-130): the query q1 (B, H, 1, D) at position t-1
+    over the t cached keys, with the carried selection state (B, t) subtracted from its logits;
+    returns (out (B, H, 1, D), the state with head 0's own selection of keys [E, t-1) added)."""
+    t = k.shape[2]
+    raw = raw_logits(q1, k)                                          # (B, H, 1, t)
+    out = torch.softmax(raw - state[:, None, None, :t], dim=-1) @ v
+    own = torch.clamp(raw[:, 0, 0], min=0)
+    own[:, :exempt] = 0
+    own[:, t - 1] = 0
+    new_state = state.clone()
+    new_state[:, :t] += own
+    return out, new_state
+
+
 def decode_steps(q, k, v, prompt: int, exempt: int = 1):
-    """Rows [prompt, T) computed one query at a time from the selection state after the prompt
-    (reference mixers.py:105-130). Returns (out_rows, final state)."""
+    """Rows [prompt, T) computed one query at a time (decode_step) from the selection state after
+    the prompt (reference mixers.py:105-130). Returns (out_rows, final state)."""
     _, state = prefill_chunks(q[:, :, :prompt], k[:, :, :prompt], v[:, :, :prompt], prompt, exempt)
     bsz, heads, t, d = q.shape
     state = torch.cat([state, torch.zeros(bsz, t - prompt, dtype=q.dtype)], dim=1)
     outs = []
     for i in range(prompt, t):
-        raw = raw_logits(q[:, :, i:i + 1], k[:, :, : i + 1])          # (B, H, 1, i+1)
-        outs.append(torch.softmax(raw - state[:, None, None, : i + 1], dim=-1) @ v[:, :, : i + 1])
-        own = torch.clamp(raw[:, 0, 0], min=0)
-        own[:, :exempt] = 0
-        own[:, i] = 0
-        state[:, : i + 1] += own
+        out, state = decode_step(q[:, :, i:i + 1], k[:, :, : i + 1], v[:, :, : i + 1], state, exempt)
+        outs.append(out)
     return torch.cat(outs, dim=2), state
 
 

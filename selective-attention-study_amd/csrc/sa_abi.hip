@@ -21,7 +21,7 @@ using namespace sa_host;
 
 extern "C" {
 
-int sa_abi_version(void) { return 2; }
+int sa_abi_version(void) { return 3; }
 
 int sa_timing_enable(int on) {
   TimingRegistry& r = timing();
@@ -117,6 +117,28 @@ int sa_backward(const void* q, const void* k, const void* v, const float* out, c
   const BwdCall c{q,  k,  v,  out, dout, rmax, rden, carry, dq, dk, dv, workspace, (int)nseq, (int)heads, (int)t,
                   scale, exempt, group, grad_dtype, (int)head_dim, static_cast<hipStream_t>(stream)};
   return dtype == SA_DTYPE_BF16 ? backward_bf16(c) : backward_f32(c);
+}
+
+int64_t sa_decode_workspace_bytes(int64_t nseq, int64_t heads, int64_t t, int64_t head_dim) {
+  if (!valid_dims(nseq, heads, t) || head_dim < 1) return -1;
+  return decode_workspace_bytes(nseq, heads, t, head_dim);
+}
+
+int sa_decode(const void* q, const void* k, const void* v, float* out, float* selected, int64_t state_ld,
+              void* workspace, int64_t workspace_bytes, int64_t nseq, int64_t heads, int64_t groups, int64_t t,
+              int64_t kv_stride, int64_t head_dim, float scale, int dtype, int exempt, void* stream) {
+  if (!valid_dims(nseq, heads, t) || groups < 1 || heads % groups != 0 || exempt < 1) return SA_ERR_ARGUMENT;
+  if (!q || !k || !v || !out || !selected || !workspace || state_ld < t) return SA_ERR_ARGUMENT;
+  if (!(scale > 0.f) || !(scale < INFINITY)) return SA_ERR_ARGUMENT;
+  if (dtype != SA_DTYPE_BF16 && dtype != SA_DTYPE_F32) return SA_ERR_DTYPE;
+  if (head_dim != 32 && head_dim != 64 && head_dim != 128) return SA_ERR_HEAD_DIM;
+  if (kv_stride == 0) kv_stride = t * head_dim;
+  if (kv_stride < t * head_dim || kv_stride % 8 != 0) return SA_ERR_ARGUMENT;
+  if (workspace_bytes < sa_decode_workspace_bytes(nseq, heads, t, head_dim)) return SA_ERR_WORKSPACE;
+  const DecCall c{q,         k,          v,           out,    selected,  state_ld, workspace,
+                  (int)nseq, (int)heads, (int)groups, (int)t, kv_stride, scale,    exempt,
+                  (int)head_dim, static_cast<hipStream_t>(stream)};
+  return dtype == SA_DTYPE_BF16 ? decode_bf16(c) : decode_f32(c);
 }
 
 }  // extern "C"

@@ -8,5 +8,6 @@ namespace sa_host {
 
 int forward_f32(const FwdCall& c) { return forward_entry<OpF32>(c); }
 int backward_f32(const BwdCall& c) { return backward_entry<OpF32>(c); }
+int decode_f32(const DecCall& c) { return decode_entry<OpF32>(c); }
 
 }  // namespace sa_host

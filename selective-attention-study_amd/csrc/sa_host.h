@@ -158,9 +158,34 @@ struct BwdCall {
   hipStream_t st;
 };
 
+// One sa_decode call after its checks.
+struct DecCall {
+  const void *q, *k, *v;
+  float *out, *selected;
+  int64_t state_ld;
+  void* ws;
+  int nseq, heads, groups, t;
+  int64_t kvs;
+  float scale;
+  int exempt, head_dim;
+  hipStream_t st;
+};
+
+// Workspace of sa_decode: the partials of (nseq*heads, chunks of 256 keys or more) fp32 maxima,
+// sums (each padded to a multiple of 4) and D-wide outputs, then the updated selection,
+// (nseq*groups, t) fp32 (groups <= heads).
+inline int64_t decode_partials_floats(int64_t nseq, int64_t heads, int64_t t, int64_t D) {
+  return align_up(nseq * heads * cdiv(t, 256), 4) * (D + 2);
+}
+inline int64_t decode_workspace_bytes(int64_t nseq, int64_t heads, int64_t t, int64_t D) {
+  return align_up((decode_partials_floats(nseq, heads, t, D) + nseq * heads * t) * 4, 256);
+}
+
 SA_HIDDEN int forward_bf16(const FwdCall& c);    // sa_bf16.hip
 SA_HIDDEN int backward_bf16(const BwdCall& c);
 SA_HIDDEN int forward_f32(const FwdCall& c);     // sa_f32.hip
 SA_HIDDEN int backward_f32(const BwdCall& c);
+SA_HIDDEN int decode_bf16(const DecCall& c);
+SA_HIDDEN int decode_f32(const DecCall& c);
 
 }  // namespace sa_host

@@ -1635,6 +1635,293 @@ __global__ __launch_bounds__(NTHREADS) void bwd_finish_kernel(
 
 
 // ---------------------------------------------------------------------------------------------
+// Decode step: one new query per head (position t-1) over a key cache of t keys. HBM-bound: every
+// cached K and V row is read once. grid (ceil(t / chunk), nseq * heads): a workgroup takes one
+// head over `chunk` keys (a multiple of 256 the host picks so that the grid fills the chip),
+// wavefront w the keys [w chunk/4, (w+1) chunk/4) of that range, DEC_STEP keys at a time.
+//
+// Lane layout: lane = (row slot kq, column slice dc), LPK = D / (elements per 16 bytes) lanes per
+// cached row, so one 16-byte load instruction reads 64 / LPK whole rows, contiguous in HBM. A lane
+// holds its slice of q and, per step, NR rows of K and the same NR rows of V (both issued before
+// any arithmetic). The NR partial dot products reduce over the LPK lanes of a row by a
+// reduce-scatter (log2 NR exchange rounds that halve the values a lane carries), after which lane
+// (kq, dc) holds the full logit of row slot kq of load dc / (LPK / NR). The wavefront then takes
+// the step's maximum, rescales its running output when the maximum rises, passes the
+// probabilities through LDS to the lanes holding the V rows, and adds p_j v_j into each lane's
+// column slice. The wavefronts' partials (max, sum, output) merge in LDS; one partial per
+// workgroup goes to the workspace. The group's selector head writes the updated selection to the
+// workspace's state rows; decode_finish_kernel merges the partials and copies the state rows over
+// the caller's state after every head has read the old one (a kernel boundary later).
+
+template <typename E, int D>
+struct DecLayout {
+  static constexpr int EPC = 16 / (int)sizeof(E);   // elements per 16-byte load
+  static constexpr int LPK = D / EPC;                // lanes per cached row
+  static constexpr int KPI = 64 / LPK;               // rows per load instruction
+  static constexpr int NR = LPK < 8 ? LPK : 8;       // rows per lane per step (K and V each)
+  static constexpr int DUP = LPK / NR;               // lanes holding one logit after the reduction
+  static constexpr int STEP = KPI * NR;              // keys per wavefront step
+};
+
+__device__ __forceinline__ float wave_max(float x) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) x = fmaxf(x, __shfl_xor(x, o));
+  return x;
+}
+__device__ __forceinline__ float wave_sum(float x) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) x += __shfl_xor(x, o);
+  return x;
+}
+template <typename E>
+__device__ __forceinline__ float to_f32(E x) {
+  if constexpr (sizeof(E) == 2) return __uint_as_float(((uint32_t)x) << 16);
+  else return x;
+}
+
+template <typename E, int D>
+__global__ __launch_bounds__(NTHREADS) void decode_partial_kernel(
+    const E* __restrict__ q, const E* __restrict__ k, const E* __restrict__ v, const float* __restrict__ selected,
+    int64_t state_ld, float* __restrict__ pm, float* __restrict__ pl, float* __restrict__ po,
+    float* __restrict__ next_state, int heads, int groups, int t, int64_t kvs, int exempt, float scale, int chunk,
+    int nchunk) {
+  using L = DecLayout<E, D>;
+  constexpr int EPC = L::EPC, LPK = L::LPK, KPI = L::KPI, NR = L::NR, DUP = L::DUP, STEP = L::STEP;
+  union Row {
+    uint4 u;
+    E e[EPC];
+  };
+  __shared__ __align__(16) float sP[NWAVES][STEP];
+  __shared__ float sPart[NWAVES][D + 2];
+
+  const int cidx = blockIdx.x;
+  const int64_t row = blockIdx.y;             // b * heads + head
+  const int per = heads / groups;
+  const int b = (int)(row / heads), hd = (int)(row % heads);
+  const int64_t sg = (int64_t)b * groups + hd / per;
+  const bool selector = (hd % per) == 0;
+  const int tid = threadIdx.x, lane = tid & 63, wave = wave_id();
+  const int kq = lane / LPK, dc = lane % LPK;
+  const int ri = dc / DUP;                    // after the reduction: the logit of row kq of load ri
+  const bool owner = dc % DUP == 0;           // one lane per logit writes it
+  const int wkeys = chunk / NWAVES;
+  const int kw0 = cidx * chunk + wave * wkeys;
+  const int kw_end = min(kw0 + wkeys, t);
+  const float* selrow = selected + sg * state_ld;
+  float* nextrow = next_state + sg * t;
+
+  float qf[EPC];
+  {
+    Row qq;
+    qq.u = *reinterpret_cast<const uint4*>(q + row * D + EPC * dc);
+#pragma unroll
+    for (int e = 0; e < EPC; ++e) qf[e] = to_f32(qq.e[e]) * scale;
+  }
+  const E* kh = k + row * kvs + EPC * dc;
+  const E* vh = v + row * kvs + EPC * dc;
+  float m = -INFINITY, l = 0.f, o[EPC];
+#pragma unroll
+  for (int e = 0; e < EPC; ++e) o[e] = 0.f;
+
+  for (int kw = kw0; kw < kw_end; kw += STEP) {
+    Row kr[NR], vr[NR];
+#pragma unroll
+    for (int i = 0; i < NR; ++i) {
+      const int jj = min(kw + i * KPI + kq, t - 1);
+      kr[i].u = *reinterpret_cast<const uint4*>(kh + (int64_t)jj * D);
+    }
+#pragma unroll
+    for (int i = 0; i < NR; ++i) {
+      const int jj = min(kw + i * KPI + kq, t - 1);
+      vr[i].u = *reinterpret_cast<const uint4*>(vh + (int64_t)jj * D);
+    }
+    const int j = kw + ri * KPI + kq;         // this lane's logit after the reduction
+    const bool jok = j < t;
+    const float sel = jok ? selrow[j] : 0.f;
+    float a[NR];
+#pragma unroll
+    for (int i = 0; i < NR; ++i) {
+      float s = 0.f;
+#pragma unroll
+      for (int e = 0; e < EPC; ++e) s = fmaf(qf[e], to_f32(kr[i].e[e]), s);
+      a[i] = s;
+    }
+    // reduce-scatter over the row's lanes: the round with lane bit `s` keeps the upper half of the
+    // values on lanes with the bit set, the lower half on the others, and adds the partner's copy
+#pragma unroll
+    for (int half = NR / 2, s = LPK / 2; half >= 1; half >>= 1, s >>= 1) {
+      const bool up = (lane & s) != 0;
+#pragma unroll
+      for (int i = 0; i < half; ++i) {
+        const float send = up ? a[i] : a[i + half];
+        const float keep = up ? a[i + half] : a[i];
+        a[i] = keep + __shfl_xor(send, s);
+      }
+    }
+#pragma unroll
+    for (int s = DUP / 2; s >= 1; s >>= 1) a[0] += __shfl_xor(a[0], s);
+    const float raw = a[0];
+    if (selector && owner && j >= exempt && j < t - 1) nextrow[j] = sel + fmaxf(raw, 0.f);
+    const float z = jok ? (raw - sel) * LOG2E : -INFINITY;
+    const float m_new = fmaxf(m, wave_max(z));   // finite: a step's first key is < t
+    const float alpha = fast_exp2(m - m_new);    // 0 on the first step (m = -inf)
+    const float p = jok ? fast_exp2(z - m_new) : 0.f;
+    l = fmaf(l, alpha, owner ? p : 0.f);         // per lane; summed over the wavefront at the end
+#pragma unroll
+    for (int e = 0; e < EPC; ++e) o[e] *= alpha;
+    m = m_new;
+    if (owner) sP[wave][kq * NR + ri] = p;
+    lds_wave_sync();
+    float pr[NR];
+#pragma unroll
+    for (int i = 0; i < NR; i += 4) {
+      const float4 p4 = *reinterpret_cast<const float4*>(&sP[wave][kq * NR + i]);
+      pr[i] = p4.x;
+      pr[i + 1] = p4.y;
+      pr[i + 2] = p4.z;
+      pr[i + 3] = p4.w;
+    }
+    lds_wave_sync();   // sP is rewritten next step
+#pragma unroll
+    for (int i = 0; i < NR; ++i)
+#pragma unroll
+      for (int e = 0; e < EPC; ++e) o[e] = fmaf(pr[i], to_f32(vr[i].e[e]), o[e]);
+  }
+  l = wave_sum(l);
+#pragma unroll
+  for (int sh = LPK; sh < 64; sh <<= 1)
+#pragma unroll
+    for (int e = 0; e < EPC; ++e) o[e] += __shfl_xor(o[e], sh);
+  if (kq == 0) {
+#pragma unroll
+    for (int e = 0; e < EPC; ++e) sPart[wave][2 + EPC * dc + e] = o[e];
+  }
+  if (lane == 0) {
+    sPart[wave][0] = m;   // -inf for a wavefront with no key (its l and o are 0)
+    sPart[wave][1] = l;
+  }
+  __syncthreads();
+  // merge the wavefronts' partials: wavefront 0, lanes over D + 2
+  if (wave == 0) {
+    float mx = -INFINITY;
+#pragma unroll
+    for (int w = 0; w < NWAVES; ++w) mx = fmaxf(mx, sPart[w][0]);
+    const int64_t slot = row * nchunk + cidx;
+    for (int c = lane; c < D + 2; c += 64) {
+      float acc = 0.f;
+#pragma unroll
+      for (int w = 0; w < NWAVES; ++w) {
+        const float wt = sPart[w][0] == -INFINITY ? 0.f : fast_exp2(sPart[w][0] - mx);
+        acc = fmaf(wt, sPart[w][c], acc);
+      }
+      if (c == 0) pm[slot] = mx;
+      else if (c == 1) pl[slot] = acc;
+      else po[slot * D + c - 2] = acc;
+    }
+  }
+}
+
+// Blocks [0, rows): out[row] = the row's partials merged, sum_p 2^(m_p - M) o_p / sum_p 2^(m_p - M)
+// l_p. Thread i first takes the maxima and sums of partials i, i + 256, ... (the weights go to LDS),
+// then thread (slot, column quad) the output quads of partials slot, slot + 1024/D, ..., a batch of
+// DEC_FIN_UNROLL loads in flight at a time; slots reduce over lanes and then over wavefronts.
+// Blocks from `rows` on: selected[g][j] = the selector heads' updates (rows of t in next_state),
+// exempt <= j < t - 1, `sblocks` blocks of 1024 keys per state row.
+constexpr int DEC_FIN_UNROLL = 8;
+constexpr int DEC_FIN_MAXPARTS = 4096;   // LDS weights of one row: nparts <= this
+
+template <int D>
+__global__ __launch_bounds__(NTHREADS) void decode_finish_kernel(
+    const float* __restrict__ pm, const float* __restrict__ pl, const float* __restrict__ po, float* __restrict__ out,
+    int nparts, int rows, float* __restrict__ selected, const float* __restrict__ next_state, int64_t state_ld, int t,
+    int exempt, int sblocks) {
+  constexpr int QPP = D / 4;               // float4 quads per partial
+  constexpr int SLOTS = NTHREADS / QPP;    // partials in flight per load instruction
+  const int tid = threadIdx.x, lane = tid & 63, wave = wave_id();
+  if ((int)blockIdx.x >= rows) {
+    const int s = (int)blockIdx.x - rows;
+    const int64_t g = s / sblocks;
+    const int j0 = (s % sblocks) * (4 * NTHREADS);
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int j = j0 + u * NTHREADS + tid;
+      if (j >= exempt && j < t - 1) selected[g * state_ld + j] = next_state[g * t + j];
+    }
+    return;
+  }
+  __shared__ float sW[DEC_FIN_MAXPARTS];
+  __shared__ float sRed[NWAVES];
+  __shared__ float4 sO[NWAVES][QPP];
+  const int64_t row = blockIdx.x;
+  const float* rm = pm + row * nparts;
+  const float* rl = pl + row * nparts;
+  const float4* ro = reinterpret_cast<const float4*>(po + row * nparts * (int64_t)D);
+
+  float mx = -INFINITY;
+  for (int i = tid; i < nparts; i += NTHREADS) {
+    const float m = rm[i];
+    sW[i] = m;
+    mx = fmaxf(mx, m);
+  }
+  mx = wave_max(mx);
+  if (lane == 0) sRed[wave] = mx;
+  __syncthreads();
+  mx = fmaxf(fmaxf(sRed[0], sRed[1]), fmaxf(sRed[2], sRed[3]));   // finite: every partial has a key
+  __syncthreads();   // sRed is reused below
+  float l = 0.f;
+  for (int i = tid; i < nparts; i += NTHREADS) {
+    const float w = fast_exp2(sW[i] - mx);
+    sW[i] = w;
+    l = fmaf(w, rl[i], l);
+  }
+  l = wave_sum(l);
+  if (lane == 0) sRed[wave] = l;
+  __syncthreads();
+  l = sRed[0] + sRed[1] + sRed[2] + sRed[3];
+
+  const int slot = tid / QPP, cq = tid % QPP;
+  float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+  for (int i0 = slot; i0 < nparts; i0 += SLOTS * DEC_FIN_UNROLL) {
+    float4 x[DEC_FIN_UNROLL];
+#pragma unroll
+    for (int u = 0; u < DEC_FIN_UNROLL; ++u) {
+      const int i = i0 + u * SLOTS;
+      x[u] = i < nparts ? ro[(int64_t)i * QPP + cq] : make_float4(0.f, 0.f, 0.f, 0.f);
+    }
+#pragma unroll
+    for (int u = 0; u < DEC_FIN_UNROLL; ++u) {
+      const int i = i0 + u * SLOTS;
+      const float w = i < nparts ? sW[i] : 0.f;
+      acc.x = fmaf(w, x[u].x, acc.x);
+      acc.y = fmaf(w, x[u].y, acc.y);
+      acc.z = fmaf(w, x[u].z, acc.z);
+      acc.w = fmaf(w, x[u].w, acc.w);
+    }
+  }
+#pragma unroll
+  for (int sh = QPP; sh < 64; sh <<= 1) {
+    acc.x += __shfl_xor(acc.x, sh);
+    acc.y += __shfl_xor(acc.y, sh);
+    acc.z += __shfl_xor(acc.z, sh);
+    acc.w += __shfl_xor(acc.w, sh);
+  }
+  if (lane < QPP) sO[wave][lane] = acc;
+  __syncthreads();
+  if (tid < QPP) {
+    float4 o = sO[0][tid];
+#pragma unroll
+    for (int w = 1; w < NWAVES; ++w) {
+      o.x += sO[w][tid].x;
+      o.y += sO[w][tid].y;
+      o.z += sO[w][tid].z;
+      o.w += sO[w][tid].w;
+    }
+    const float inv = 1.f / l;
+    reinterpret_cast<float4*>(out + row * D)[tid] = make_float4(o.x * inv, o.y * inv, o.z * inv, o.w * inv);
+  }
+}
+
+// ---------------------------------------------------------------------------------------------
 // Host side: launch sequences of one storage dtype and head dim.
 
 template <class OP, int D>
@@ -1776,6 +2063,55 @@ int backward_impl(const void* q_, const void* k_, const void* v_, const float* o
                        static_cast<uint16_t*>(dq_), static_cast<uint16_t*>(dk_), static_cast<uint16_t*>(dv_), H,
                        (int64_t)T * D, total, scale);
   return launch_status();
+}
+
+#ifndef SA_DEC_CHUNK
+#define SA_DEC_CHUNK 0   // keys per decode workgroup; 0: decode_chunk() picks
+#endif
+
+// Keys per decode workgroup: the smallest power of two from 256 up that keeps the grid at or under
+// 2048 workgroups (8 per CU) up to 4096 keys, and beyond that as far as a row's partials need to
+// fit decode_finish_kernel's LDS.
+inline int decode_chunk(int64_t rows, int64_t t) {
+  if (SA_DEC_CHUNK) return SA_DEC_CHUNK;
+  int64_t chunk = 256;
+  while ((chunk < 4096 && rows * cdiv(t, chunk) > 2048) || cdiv(t, chunk) > DEC_FIN_MAXPARTS) chunk *= 2;
+  return (int)chunk;
+}
+
+template <class OP, int D>
+int decode_impl(const DecCall& c) {
+  using elem = typename OP::elem;
+  const int64_t rows = (int64_t)c.nseq * c.heads;
+  const int chunk = decode_chunk(rows, c.t);
+  const int nchunk = (int)cdiv(c.t, chunk);
+  if (nchunk > DEC_FIN_MAXPARTS) return SA_ERR_ARGUMENT;
+  // workspace: maxima, sums (rows * nchunk each, padded to 4) and outputs (rows * nchunk * D) of the
+  // partials, then the updated selection rows
+  const int64_t np = align_up(rows * nchunk, 4);
+  float* pm = static_cast<float*>(c.ws);
+  float* pl = pm + np;
+  float* po = pl + np;
+  float* next_state = pm + decode_partials_floats(c.nseq, c.heads, c.t, D);
+  dim3 g1((unsigned)nchunk, (unsigned)rows);
+  {
+    TimedLaunch timed(SA_KERNEL_DECODE, c.st);
+    hipLaunchKernelGGL((decode_partial_kernel<elem, D>), g1, dim3(NTHREADS), 0, c.st, static_cast<const elem*>(c.q),
+                       static_cast<const elem*>(c.k), static_cast<const elem*>(c.v), c.selected, c.state_ld, pm, pl,
+                       po, next_state, c.heads, c.groups, c.t, c.kvs, c.exempt, c.scale, chunk, nchunk);
+  }
+  const int sblocks = (int)cdiv(c.t, 4 * NTHREADS);
+  const int64_t nblocks = rows + (int64_t)c.nseq * c.groups * sblocks;
+  hipLaunchKernelGGL((decode_finish_kernel<D>), dim3((unsigned)nblocks), dim3(NTHREADS), 0, c.st, pm, pl, po, c.out,
+                     nchunk, (int)rows, c.selected, next_state, c.state_ld, c.t, c.exempt, sblocks);
+  return launch_status();
+}
+
+template <class OP>
+int decode_entry(const DecCall& c) {
+  if (c.head_dim == 32) return decode_impl<OP, 32>(c);
+  if (c.head_dim == 64) return decode_impl<OP, 64>(c);
+  return decode_impl<OP, 128>(c);
 }
 
 template <class OP>

@@ -24,6 +24,7 @@ KERNEL_FORWARD = 0
 KERNEL_BACKWARD = 1
 KERNEL_SELECTION = 2
 KERNEL_BACKWARD_DQ = 3
+KERNEL_DECODE = 4
 
 # Every function the header declares, with its ctypes signature.
 _P = ctypes.c_void_p
@@ -42,6 +43,8 @@ SIGNATURES = {
     "sa_backward_workspace_bytes": (_I64, [_I64, _I64, _I64, _I64, _I, _I]),
     "sa_backward": (_I, [_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _I64,
                          _I64, _I64, _I64, _I64, _F, _I, _I, _I, _I, _P]),
+    "sa_decode_workspace_bytes": (_I64, [_I64, _I64, _I64, _I64]),
+    "sa_decode": (_I, [_P, _P, _P, _P, _P, _I64, _P, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _F, _I, _I, _P]),
 }
 
 _lock = threading.Lock()

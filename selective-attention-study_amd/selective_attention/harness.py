@@ -15,6 +15,7 @@ random-init weights. Times are HIP events around whole steps after warm-up.
     python -m selective_attention.harness c3 [--geometry d768|d1024] [--steps K] [--warmup W]
     python -m selective_attention.harness c4 [--tokens 131072] [--chunk 16384]
     python -m selective_attention.harness c5
+    python -m selective_attention.harness decode [--tokens 131072]   (one decode step's HBM rate)
     python -m selective_attention.harness copy      (reference copy for rocprofv3 byte counters)
 """
 
@@ -27,7 +28,7 @@ import sys
 
 import torch
 
-from . import kernels
+from . import _lib, kernels
 from .model import ModelConfig, SelectiveLM
 
 GPT2_VOCAB = 50257
@@ -155,6 +156,37 @@ def perhead_rate(batch: int = 2, heads: int = 16, seq: int = 32768, head_dim: in
             "ms_per_step": ms, "tflops": tf, "frac_of_peak": tf / PEAK_BF16_TFLOPS}
 
 
+def decode_rate(t: int = 131072, batch: int = 1, heads: int = 16, head_dim: int = 64, steps: int = 50,
+                warmup: int = 5) -> dict:
+    """One cached decode step of one layer (the newest query of every head over t cached keys,
+    bf16 cache, head 0 selecting): HBM bandwidth of the step against the 8 TB/s roof. Bytes: the K
+    and V rows read once, the selection state read and written (fp32). `ms` is the whole call
+    (host work of the wrapper included, which bounds small caches); `kernel_ms` the cache-reading
+    kernel alone, from HIP events around it."""
+    dev = torch.device("cuda")
+    g = torch.Generator(device=dev).manual_seed(6)
+    k, v = (torch.randn(batch, heads, t, head_dim, device=dev, generator=g).bfloat16() for _ in range(2))
+    q = torch.randn(batch, heads, head_dim, device=dev, generator=g).bfloat16()
+    sel = torch.rand(batch, 1, t, device=dev, generator=g)
+
+    def step():
+        kernels.selective_attention_decode(q, k, v, sel)
+
+    ms = _timed(step, steps, warmup)
+    _lib.timing_enable(True)
+    for _ in range(steps):
+        step()
+    kms, launches = _lib.timing_read(_lib.KERNEL_DECODE)
+    _lib.timing_enable(False)
+    kms /= max(launches, 1)
+    nbytes = 2 * batch * heads * t * head_dim * 2 + 2 * batch * t * 4
+    gbs = nbytes / (ms * 1e-3) / 1e9
+    return {"config": f"decode step, B={batch} H={heads} t={t} D={head_dim} bf16 cache, shared selection",
+            "ms": ms, "bytes": nbytes, "gb_per_s": gbs, "frac_of_hbm_peak": gbs / 8000.0,
+            "tokens_per_s": batch / (ms * 1e-3), "kernel_ms": kms,
+            "kernel_gb_per_s": nbytes / (kms * 1e-3) / 1e9}
+
+
 def copy_probe(mib: int = 1024, reps: int = 3) -> dict:
     """A plain device-to-device copy of `mib` MiB, `reps` times: the reference point that scales the
     FETCH_SIZE / WRITE_SIZE counters of rocprofv3 (each copy reads and writes exactly `mib` MiB)."""
@@ -167,7 +199,7 @@ def copy_probe(mib: int = 1024, reps: int = 3) -> dict:
 
 def main(argv=None) -> int:
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
-    ap.add_argument("which", choices=["c3", "c4", "c5", "copy"])
+    ap.add_argument("which", choices=["c3", "c4", "c5", "decode", "copy"])
     ap.add_argument("--geometry", default=None, choices=sorted(GEOMETRIES))
     ap.add_argument("--steps", type=int, default=None)
     ap.add_argument("--warmup", type=int, default=None)
@@ -186,6 +218,8 @@ def main(argv=None) -> int:
                            **({"reps": a.steps} if a.steps else {}), **({"warmup": a.warmup} if a.warmup is not None else {}))
     elif a.which == "c5":
         res = perhead_rate(**kw)
+    elif a.which == "decode":
+        res = decode_rate(t=a.tokens, **kw)
     else:
         res = copy_probe()
     print(json.dumps(res), flush=True)

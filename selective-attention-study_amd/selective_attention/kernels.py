@@ -311,6 +311,64 @@ def selective_attention_prefill(
     return out[..., :head_dim].reshape(batch, heads, tc, head_dim)
 
 
+def selective_attention_decode(
+    q: torch.Tensor,
+    k: torch.Tensor,
+    v: torch.Tensor,
+    selected: torch.Tensor,
+    exempt: int = 1,
+) -> torch.Tensor:
+    """One cached decode step through the HIP kernel (the reference runs this step as PyTorch ops,
+    mixers.py:115-130): the newest query of every head, at position t-1, attends over the t cached
+    keys (its own included) with the carried selection subtracted from its logits; then the
+    selector head of every group adds this query's own selection to ``selected`` (in place).
+
+    q: (B, H, 1, D) or (B, H, D). k, v: (B, H, t, D) (a slice of a preallocated cache is used in
+    place). selected: (B, G, L) fp32, L >= t, G dividing H: group g's heads are g*H/G ... and its
+    selector is the first of them (G = 1: head 0 selects for every head; G = H: every head for
+    itself). Logits, softmax and sums are fp32 on the upcast operands, as the reference's step.
+    Returns fp32 (B, H, D).
+    """
+
+    if q.dim() == 4:
+        if q.shape[2] != 1:
+            raise ValueError(f"decode takes one query per head; got q of shape {tuple(q.shape)}")
+        q = q[:, :, 0]
+    if q.dim() != 3 or k.dim() != 4 or k.shape != v.shape or q.shape[:2] != k.shape[:2] or q.shape[-1] != k.shape[-1]:
+        raise ValueError(f"q (B, H, D) and k, v (B, H, t, D) must all be with matching B, H, D; "
+                         f"got {tuple(q.shape)}, {tuple(k.shape)}, {tuple(v.shape)}")
+    check_inputs(k, k, v)
+    check_inputs(q[:, :, None], q[:, :, None], q[:, :, None])
+    exempt = _check_exempt(exempt)
+    batch, heads, t, head_dim = k.shape
+    if (selected.dim() != 3 or selected.shape[0] != batch or heads % selected.shape[1] != 0
+            or selected.shape[2] < t or selected.dtype != torch.float32 or selected.device != q.device
+            or selected.stride(2) != 1 or selected.stride(0) != selected.shape[1] * selected.stride(1)):
+        raise ValueError(f"selected must be a (B, G, >= {t}) fp32 tensor with G dividing H, rows a fixed "
+                         f"stride apart, on q's device")
+    groups = selected.shape[1]
+    lib = _lib.load()
+    # bf16 caches are read as bf16; anything else as fp32 (exact for fp16 and fp32 values)
+    dtype = _lib.DTYPE_BF16 if k.dtype == torch.bfloat16 and v.dtype == torch.bfloat16 else _lib.DTYPE_F32
+    n = batch * heads
+    kdim = _kernel_dim(head_dim)
+    dev = q.device
+    qs = _storage(q[:, :, None], n, dtype, kdim)
+    ks, kstride = _kv_storage(k, n, dtype, kdim, True)
+    vs, vstride = _kv_storage(v, n, dtype, kdim, True)
+    if kstride != vstride:
+        ks, vs = _storage(k, n, dtype, kdim), _storage(v, n, dtype, kdim)
+        kstride = t * kdim
+    out = torch.empty(n, kdim, device=dev, dtype=torch.float32)
+    ws_bytes = lib.sa_decode_workspace_bytes(batch, heads, t, kdim)
+    ws = torch.empty(max(int(ws_bytes), 1), device=dev, dtype=torch.uint8)
+    with torch.cuda.device(dev):
+        _lib.check(lib.sa_decode(qs.data_ptr(), ks.data_ptr(), vs.data_ptr(), out.data_ptr(), selected.data_ptr(),
+                                 selected.stride(1), ws.data_ptr(), ws.numel(), batch, heads, groups, t, kstride,
+                                 kdim, 1.0 / math.sqrt(head_dim), dtype, exempt, _stream(dev)))
+    return out[:, :head_dim].reshape(batch, heads, head_dim)
+
+
 class _SelectiveAttentionFn(torch.autograd.Function):
     """Autograd wrapper (reference kernels.py:608-666): forward saves the operand tensors, the fp32
     output, row statistics and CARRY; backward runs sa_backward, head 0's selection gradient

@@ -152,11 +152,17 @@ def selective_class():
 
             def step_cache(self, x1: Tensor, cache: dict) -> Tensor:
                 """One decode step (reference mixers.py:115-130): subtract the carried selection from
-                every head's logits, then add this query's own selection to the state."""
+                every head's logits, then add this query's own selection to the state. With
+                use_kernel, one HIP launch pair (kernels.selective_attention_decode); otherwise the
+                reference's PyTorch step."""
                 b = x1.shape[0]
                 q1, k1, v1 = self._split_heads(x1, offset=cache["len"])
                 t = self._append_kv(cache, k1, v1)
                 keys, vals = cache["k"][:, :, :t], cache["v"][:, :, :t]
+                if self.use_kernel:
+                    self._check_kernel(q1)
+                    y = kernels.selective_attention_decode(q1, keys, vals, cache["selected"], exempt=self.exempt)
+                    return self._merge_heads(y[:, :, None].to(x1.dtype), b, 1)
                 selected = cache["selected"][:, :, :t]                   # (B, G, t)
                 per = self.n_heads // self.groups
                 with torch.autocast(x1.device.type, enabled=False):

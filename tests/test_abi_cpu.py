@@ -47,6 +47,33 @@ def test_workspace_sizes():
     assert fw >= 16 * 64 * 16384 * 2 and fw % 256 == 0
     bw = lib.sa_backward_workspace_bytes(1, 16, 16384, 64, 0, 0)
     assert bw >= 16 * 16384 * 64 * 4 * 3    # dq, dk, dv fp32 at least
+    dw = lib.sa_decode_workspace_bytes(1, 16, 131072, 64)
+    assert dw >= 16 * (131072 // 64) * 66 * 4 and dw % 256 == 0   # one (m, l, o[64]) per 64 keys and head
+    assert lib.sa_decode_workspace_bytes(0, 16, 100, 64) < 0
+
+
+def test_decode_rejects_invalid_arguments():
+    lib = _lib.load()
+    fake = 1 << 20   # never dereferenced: validation fails first
+    args = [fake] * 5 + [128, fake, 1 << 30, 1, 4, 1, 100, 0, 64, 0.125, 0, 1, None]
+    bad = list(args)
+    bad[10] = 3          # groups does not divide heads
+    assert lib.sa_decode(*bad) == -1
+    bad = list(args)
+    bad[5] = 99          # state row shorter than t
+    assert lib.sa_decode(*bad) == -1
+    bad = list(args)
+    bad[13] = 48         # head_dim
+    assert lib.sa_decode(*bad) == -2
+    bad = list(args)
+    bad[15] = 9          # dtype
+    assert lib.sa_decode(*bad) == -3
+    bad = list(args)
+    bad[7] = 8           # workspace too small
+    assert lib.sa_decode(*bad) == -4
+    bad = list(args)
+    bad[16] = 0          # exempt
+    assert lib.sa_decode(*bad) == -1
 
 
 def test_invalid_arguments_are_rejected_before_any_launch():

@@ -141,6 +141,26 @@ def test_decode_steps_equal_single_shot():
     torch.testing.assert_close(state, sa_oracle.selection_totals(q, k), atol=1e-12, rtol=1e-10)
 
 
+def test_decode_step_from_arbitrary_state():
+    """One step from a random non-negative state, against the softmax written out per key with exp
+    and sums, and the state update written per key (head 0's relu logit on keys [E, t-1))."""
+    q, k, v = _qkv(2, 3, 17, 8, seed=15, scale=1.5)
+    g = torch.Generator().manual_seed(16)
+    state = torch.rand(2, 20, generator=g, dtype=torch.float64) * 3
+    out, new_state = sa_oracle.decode_step(q[:, :, -1:], k, v, state, exempt=2)
+    s = 1 / math.sqrt(8)
+    for b in range(2):
+        for h in range(3):
+            z = [s * float(q[b, h, -1] @ k[b, h, j]) - float(state[b, j]) for j in range(17)]
+            w = [math.exp(x - max(z)) for x in z]
+            want = sum(wj * v[b, h, j] for j, wj in enumerate(w)) / sum(w)
+            torch.testing.assert_close(out[b, h, 0], want, atol=1e-12, rtol=1e-10)
+        for j in range(20):
+            raw0 = s * float(q[b, 0, -1] @ k[b, 0, j]) if j < 17 else 0.0
+            add = max(raw0, 0.0) if 2 <= j < 16 else 0.0
+            assert abs(float(new_state[b, j]) - (float(state[b, j]) + add)) < 1e-12
+
+
 def test_per_head_equals_each_head_alone():
     """reference tests/test_selective_perhead.py:25-29"""
     q, k, v = _qkv(2, 3, 21, 8, seed=10, scale=1.5)
