@@ -1653,12 +1653,21 @@ __global__ __launch_bounds__(NTHREADS) void bwd_finish_kernel(
 // workspace's state rows; decode_finish_kernel merges the partials and copies the state rows over
 // the caller's state after every head has read the old one (a kernel boundary later).
 
+#ifndef SA_DEC_NR
+#define SA_DEC_NR 8
+#endif
+// Word 3 of a raw buffer resource on gfx950 (32-bit data format; offsets in bytes, range-checked
+// against the resource's byte count: loads past it return zero).
+constexpr int DEC_RSRC_WORD3 = 0x00020000;
+#ifndef SA_DEC_MINB
+#define SA_DEC_MINB 1
+#endif
 template <typename E, int D>
 struct DecLayout {
   static constexpr int EPC = 16 / (int)sizeof(E);   // elements per 16-byte load
   static constexpr int LPK = D / EPC;                // lanes per cached row
   static constexpr int KPI = 64 / LPK;               // rows per load instruction
-  static constexpr int NR = LPK < 8 ? LPK : 8;       // rows per lane per step (K and V each)
+  static constexpr int NR = LPK < SA_DEC_NR ? LPK : SA_DEC_NR;   // rows per lane per step (K, V each)
   static constexpr int DUP = LPK / NR;               // lanes holding one logit after the reduction
   static constexpr int STEP = KPI * NR;              // keys per wavefront step
 };
@@ -1680,7 +1689,7 @@ __device__ __forceinline__ float to_f32(E x) {
 }
 
 template <typename E, int D>
-__global__ __launch_bounds__(NTHREADS) void decode_partial_kernel(
+__global__ __launch_bounds__(NTHREADS, SA_DEC_MINB) void decode_partial_kernel(
     const E* __restrict__ q, const E* __restrict__ k, const E* __restrict__ v, const float* __restrict__ selected,
     int64_t state_ld, float* __restrict__ pm, float* __restrict__ pl, float* __restrict__ po,
     float* __restrict__ next_state, int heads, int groups, int t, int64_t kvs, int exempt, float scale, int chunk,
@@ -1717,8 +1726,13 @@ __global__ __launch_bounds__(NTHREADS) void decode_partial_kernel(
 #pragma unroll
     for (int e = 0; e < EPC; ++e) qf[e] = to_f32(qq.e[e]) * scale;
   }
-  const E* kh = k + row * kvs + EPC * dc;
-  const E* vh = v + row * kvs + EPC * dc;
+  // buffer resources over the head's t cached rows: the loads take one lane offset (row slot and
+  // column slice) plus a wavefront-uniform offset of the rows, and rows at or past t read as zero
+  constexpr int RB = D * (int)sizeof(E);   // bytes per cached row
+  const int nbytes = t * RB;               // < 2^31, checked by the host
+  const __amdgpu_buffer_rsrc_t krs = __builtin_amdgcn_make_buffer_rsrc((void*)(k + row * kvs), 0, nbytes, DEC_RSRC_WORD3);
+  const __amdgpu_buffer_rsrc_t vrs = __builtin_amdgcn_make_buffer_rsrc((void*)(v + row * kvs), 0, nbytes, DEC_RSRC_WORD3);
+  const int loff = kq * RB + EPC * dc * (int)sizeof(E);
   float m = -INFINITY, l = 0.f, o[EPC];
 #pragma unroll
   for (int e = 0; e < EPC; ++e) o[e] = 0.f;
@@ -1727,13 +1741,13 @@ __global__ __launch_bounds__(NTHREADS) void decode_partial_kernel(
     Row kr[NR], vr[NR];
 #pragma unroll
     for (int i = 0; i < NR; ++i) {
-      const int jj = min(kw + i * KPI + kq, t - 1);
-      kr[i].u = *reinterpret_cast<const uint4*>(kh + (int64_t)jj * D);
+      const auto x = __builtin_amdgcn_raw_buffer_load_b128(krs, loff, (kw + i * KPI) * RB, 0);
+      kr[i].u = make_uint4(x[0], x[1], x[2], x[3]);
     }
 #pragma unroll
     for (int i = 0; i < NR; ++i) {
-      const int jj = min(kw + i * KPI + kq, t - 1);
-      vr[i].u = *reinterpret_cast<const uint4*>(vh + (int64_t)jj * D);
+      const auto x = __builtin_amdgcn_raw_buffer_load_b128(vrs, loff, (kw + i * KPI) * RB, 0);
+      vr[i].u = make_uint4(x[0], x[1], x[2], x[3]);
     }
     const int j = kw + ri * KPI + kq;         // this lane's logit after the reduction
     const bool jok = j < t;
@@ -1749,12 +1763,16 @@ __global__ __launch_bounds__(NTHREADS) void decode_partial_kernel(
     // reduce-scatter over the row's lanes: the round with lane bit `s` keeps the upper half of the
     // values on lanes with the bit set, the lower half on the others, and adds the partner's copy
 #pragma unroll
-    for (int half = NR / 2, s = LPK / 2; half >= 1; half >>= 1, s >>= 1) {
-      const bool up = (lane & s) != 0;
+    for (int st = 1; st < NR; st <<= 1) {   // st = 1, 2, ..., NR/2: constant trip count, unrolled
+      const int half = NR / (2 * st), s = LPK / (2 * st);
+      // all-ones on lanes with the bit: a bitwise select (a ?: on the array elements becomes a
+      // dynamically indexed read of the array)
+      const uint32_t up = (lane & s) ? 0xffffffffu : 0u;
 #pragma unroll
       for (int i = 0; i < half; ++i) {
-        const float send = up ? a[i] : a[i + half];
-        const float keep = up ? a[i + half] : a[i];
+        const uint32_t lo = __float_as_uint(a[i]), hi = __float_as_uint(a[i + half]);
+        const float send = __uint_as_float((lo & up) | (hi & ~up));
+        const float keep = __uint_as_float((hi & up) | (lo & ~up));
         a[i] = keep + __shfl_xor(send, s);
       }
     }
@@ -2085,7 +2103,8 @@ int decode_impl(const DecCall& c) {
   const int64_t rows = (int64_t)c.nseq * c.heads;
   const int chunk = decode_chunk(rows, c.t);
   const int nchunk = (int)cdiv(c.t, chunk);
-  if (nchunk > DEC_FIN_MAXPARTS) return SA_ERR_ARGUMENT;
+  if (nchunk > DEC_FIN_MAXPARTS || (int64_t)c.t * D * (int64_t)sizeof(elem) >= ((int64_t)1 << 31))
+    return SA_ERR_ARGUMENT;
   // workspace: maxima, sums (rows * nchunk each, padded to 4) and outputs (rows * nchunk * D) of the
   // partials, then the updated selection rows
   const int64_t np = align_up(rows * nchunk, 4);
