@@ -126,7 +126,7 @@ int sa_backward(const void* q, const void* k, const void* v, const float* out, c
                 int64_t nseq, int64_t heads, int64_t t, int64_t head_dim, float scale, int dtype,
                 int grad_dtype, int exempt, int group, void* stream);
 
-/* Bytes of scratch sa_decode needs (per-chunk partial softmax sums) for t cached keys. */
+/* Bytes of scratch sa_decode needs (per-chunk partial softmax sums, the new state rows) for t keys. */
 int64_t sa_decode_workspace_bytes(int64_t nseq, int64_t heads, int64_t t, int64_t head_dim);
 
 /*
@@ -142,6 +142,9 @@ int64_t sa_decode_workspace_bytes(int64_t nseq, int64_t heads, int64_t t, int64_
  *   groups     selector groups per sequence: 1 = head 0 selects for every head (the shared
  *              variant), heads = every head selects for itself; heads % groups == 0
  * Logits, softmax and sums are fp32 on the upcast operands, as the reference's step.
+ * Limits: head_dim 32, 64 or 128; kv_stride (0 = t * head_dim) a multiple of 8; one head's t rows
+ * below 2 GiB (t * head_dim * element size < 2^31); q, k, v 16-byte aligned. Successive calls on
+ * one stream may share one workspace.
  */
 int sa_decode(const void* q, const void* k, const void* v, float* out, float* selected, int64_t state_ld,
               void* workspace, int64_t workspace_bytes, int64_t nseq, int64_t heads, int64_t groups, int64_t t,
