@@ -510,7 +510,7 @@ __global__ __launch_bounds__(NTHREADS, (fwd_min_blocks<OP, D, G>())) void fwd_ke
 
   __shared__ __attribute__((aligned(16))) elem sK[NBUF][NH][TILE * LDK];
   __shared__ __attribute__((aligned(16))) elem sVt[NBUF][G][D * LDV];
-  __shared__ __attribute__((aligned(16))) float sC[NBUF][NWAVES][TILE];   // carry rows, log2 units
+  __shared__ __attribute__((aligned(16))) float sC[NBUF][NWAVES][TILE];   // -carry rows, logit units
   constexpr int LDF = TILE + 4;
   __shared__ __attribute__((aligned(16))) float sF[NWAVES][TILE * LDF];   // each wavefront's F tile
 
@@ -561,7 +561,11 @@ __global__ __launch_bounds__(NTHREADS, (fwd_min_blocks<OP, D, G>())) void fwd_ke
     for (int db = 0; db < DB; ++db) o[g][db] = zero16();
   }
 
+  // F is kept negated and in units of the unscaled logit q.k (relu(s x) = s relu(x) for s > 0):
+  // the logit product then accumulates onto -F and yields q.k - F/s directly, and the scale (with
+  // log2 e) enters once, in the exponent's fma.
   const float sl2 = scale * LOG2E;
+  const float neg_inv_scale = -1.f / scale;
   float damp = 1.f;
   if (damp_mode != 0) {
     damp = fminf(1.f, train_len / (float)(q_abs + 1));
@@ -585,7 +589,7 @@ __global__ __launch_bounds__(NTHREADS, (fwd_min_blocks<OP, D, G>())) void fwd_ke
     const int rbw = min(qsb * NWAVES + w, NBq - 1);
     const int jj = kbase + (tid & (TILE - 1));
     const float c = carry[((int64_t)b * NBq + rbw) * Tk + min(jj, Tk - 1)];
-    nC = (jj < Tk) ? c * LOG2E : 0.f;
+    nC = (jj < Tk) ? c * neg_inv_scale : 0.f;
   };
   auto store_tile = [&](int buf) {
 #pragma unroll
@@ -615,9 +619,9 @@ __global__ __launch_bounds__(NTHREADS, (fwd_min_blocks<OP, D, G>())) void fwd_ke
       // compiler copy the output sums between register sets every tile)
       auto body = [&]() {
         // Head 0's logits as (queries x keys), lane = key kbase + n: the selection's running sum
-        // over queries then stays within the lane. F (log2 units) = the carry at the block's first
-        // query + the selection by the block's earlier queries; it returns to the (keys x queries)
-        // layout of the softmax through this wavefront's LDS rows.
+        // over queries then stays within the lane. -F (logit units) = -(the carry at the block's
+        // first query + the selection by the block's earlier queries); it returns to the
+        // (keys x queries) layout of the softmax through this wavefront's LDS rows.
         f32x16 l0t = zero16();
         {
           const elem* k0s = has_h0 ? sK[buf][0] : sK[buf][G];
@@ -628,7 +632,9 @@ __global__ __launch_bounds__(NTHREADS, (fwd_min_blocks<OP, D, G>())) void fwd_ke
         {
           f32x16 sel;
 #pragma unroll
-          for (int i = 0; i < 16; ++i) sel[i] = fmaxf(l0t[i] * sl2, 0.f);
+          // -relu as one v_med3 (fminf on a negated value, or a med3 with an infinite bound, which
+          // the compiler folds into fminf, would first be canonicalised)
+          for (int i = 0; i < 16; ++i) sel[i] = __builtin_amdgcn_fmed3f(-l0t[i], -3.0e38f, 0.f);
           if (edge) {
             // pairs exempt <= j < r; keys past the end and queries past the end hold zero rows
             const int jk = kbase + n;
@@ -667,11 +673,9 @@ __global__ __launch_bounds__(NTHREADS, (fwd_min_blocks<OP, D, G>())) void fwd_ke
 
 #pragma unroll
         for (int g = 0; g < G; ++g) {
-          f32x16 lg = zero16();
+          f32x16 lg = fs;   // the product accumulates onto -F: lg = q.k - F/s
 #pragma unroll
           for (int s = 0; s < NS; ++s) lg = OP::mma(OP::ld_std(sK[buf][g], LDK, n, h, s), qf[g][s], lg);
-#pragma unroll
-          for (int i = 0; i < 16; ++i) lg[i] = fmaf(lg[i], sl2, -fs[i]);
           if (edge) {   // keys j = kbase + crow(i, h) <= min(q_abs, Tk - 1)
             const int thr = min(q_abs, Tk - 1) - kbase - 4 * h;
 #pragma unroll
@@ -681,7 +685,7 @@ __global__ __launch_bounds__(NTHREADS, (fwd_min_blocks<OP, D, G>())) void fwd_ke
 #pragma unroll
           for (int i = 0; i < 16; ++i) zmax = fmaxf(zmax, lg[i]);
           const Halves zh = halves(zmax);
-          const float m_new = fmaxf(m[g], fmaxf(zh.lo, zh.hi));
+          const float m_new = fmaxf(m[g], fmaxf(zh.lo, zh.hi) * sl2);   // log2 units
           if (__any(m_new > m[g])) {   // some row's maximum rose: rescale what was accumulated
             const float alpha = (m_new == -INFINITY) ? 1.f : fast_exp2(m[g] - m_new);
             m[g] = m_new;
@@ -695,7 +699,7 @@ __global__ __launch_bounds__(NTHREADS, (fwd_min_blocks<OP, D, G>())) void fwd_ke
           float psum = 0.f;
 #pragma unroll
           for (int i = 0; i < 16; ++i) {
-            const float p = fast_exp2(lg[i] - mu);
+            const float p = fast_exp2(fmaf(lg[i], sl2, -mu));
             lg[i] = p;
             psum += p;
           }
@@ -863,18 +867,21 @@ struct TileMasks {
   }
 };
 
-// Head 0's selection on a tile of its raw logits l0, in log2 units: sel = relu(s log2e l0) where
-// exempt <= j < r < T, and the history F[r, j] = hist2 + sum of sel over the tile's earlier rows
-// (the running sum runs down the rows; the half-wavefronts exchange partial sums). Bit i of gate is
-// sel[i] > 0, the gate of the gradient path. `edge` (wave-uniform) marks tiles where some pair
-// fails exempt <= j < r: the mask is applied there (every tile when ALWAYS, which costs a few
-// instructions per element but no branch).
+// Head 0's selection on a tile of its raw logits l0 = q.k, in the same unscaled units (relu(s x) =
+// s relu(x) for s > 0): sel = relu(l0) where exempt <= j < r < T, and the negated history
+// fs[r, j] = nhist - sum of sel over the tile's earlier rows, nhist = -(the selection before the
+// tile) / s (the running sum runs down the rows; the half-wavefronts exchange partial sums). A
+// logit product accumulating onto fs then yields q.k - F/s. Bit i of gate is sel[i] > 0, the gate
+// of the gradient path. `edge` (wave-uniform) marks tiles where some pair fails exempt <= j < r:
+// the mask is applied there (every tile when ALWAYS, which costs a few instructions per element
+// but no branch).
 template <bool ALWAYS>
-__device__ __forceinline__ void selection_tile(const f32x16& l0, float hist2, float sl2, int h, bool edge,
+__device__ __forceinline__ void selection_tile(const f32x16& l0, float nhist, int h, bool edge,
                                                const TileMasks& mk, uint32_t& gate, f32x16& fs) {
   f32x16 sel;
+  // relu as one v_med3 (fmaxf on a product's result would first be canonicalised)
 #pragma unroll
-  for (int i = 0; i < 16; ++i) sel[i] = fmaxf(l0[i] * sl2, 0.f);
+  for (int i = 0; i < 16; ++i) sel[i] = __builtin_amdgcn_fmed3f(l0[i], 0.f, 3.0e38f);
   if (ALWAYS || edge) {
 #pragma unroll
     for (int i = 0; i < 16; ++i) sel[i] = crow(i, 0) > mk.thr_s ? sel[i] : 0.f;
@@ -882,17 +889,17 @@ __device__ __forceinline__ void selection_tile(const f32x16& l0, float hist2, fl
   gate = 0;
 #pragma unroll
   for (int i = 0; i < 16; ++i) gate |= sel[i] > 0.f ? (1u << i) : 0u;
-  float run = hist2;
+  float run = nhist;
 #pragma unroll
   for (int a = 0; a < 4; ++a) {
     const Halves g = halves(((sel[4 * a] + sel[4 * a + 1]) + sel[4 * a + 2]) + sel[4 * a + 3]);
-    float p = (h == 0) ? run : run + g.lo;   // rows 8a..8a+3 sit in the low half, 8a+4.. in the high
+    float p = (h == 0) ? run : run - g.lo;   // rows 8a..8a+3 sit in the low half, 8a+4.. in the high
 #pragma unroll
     for (int t = 0; t < 4; ++t) {
       fs[4 * a + t] = p;
-      p += sel[4 * a + t];
+      p -= sel[4 * a + t];
     }
-    run = (run + g.lo) + g.hi;
+    run = (run - g.lo) - g.hi;
   }
 }
 
@@ -916,11 +923,11 @@ __device__ __forceinline__ float gpath_tile(const f32x16& z, float u_in, uint32_
   return -nrun;
 }
 
-// P = exp2(s log2e lg - F - lse) and dz = P (dp - dbar) on a tile; lse and dbar of the tile's rows
-// come from LDS (4 consecutive rows per float4). Pairs outside j <= r, j < T are zeroed on `edge`
-// tiles (every tile when ALWAYS).
+// P = exp2(s log2e lg - lse) and dz = P (dp - dbar) on a tile, lg = q.k - F/s; lse and dbar of the
+// tile's rows come from LDS (4 consecutive rows per float4). Pairs outside j <= r, j < T are zeroed
+// on `edge` tiles (every tile when ALWAYS).
 template <bool ALWAYS>
-__device__ __forceinline__ void p_dz_tile(const f32x16& lg, const f32x16& dp, const f32x16& fs, const float* slse,
+__device__ __forceinline__ void p_dz_tile(const f32x16& lg, const f32x16& dp, const float* slse,
                                           const float* sdb, float sl2, int h, bool edge, const TileMasks& mk,
                                           f32x16& pr, f32x16& dz) {
   if constexpr (ALWAYS) {
@@ -933,7 +940,7 @@ __device__ __forceinline__ void p_dz_tile(const f32x16& lg, const f32x16& dp, co
 #pragma unroll
       for (int t = 0; t < 4; ++t) {
         const int i = 4 * a + t;
-        const float p = fast_exp2(fmaf(lg[i], sl2, -(fs[i] + lsv[t])));
+        const float p = fast_exp2(fmaf(lg[i], sl2, -lsv[t]));
         pr[i] = crow(i, 0) >= mk.thr_p ? p : 0.f;
         dz[i] = pr[i] * (dp[i] - dbs[t]);
       }
@@ -944,7 +951,7 @@ __device__ __forceinline__ void p_dz_tile(const f32x16& lg, const f32x16& dp, co
       const float4 ls = *reinterpret_cast<const float4*>(slse + 8 * a + 4 * h);
       const float lsv[4] = {ls.x, ls.y, ls.z, ls.w};
 #pragma unroll
-      for (int t = 0; t < 4; ++t) pr[4 * a + t] = fast_exp2(fmaf(lg[4 * a + t], sl2, -(fs[4 * a + t] + lsv[t])));
+      for (int t = 0; t < 4; ++t) pr[4 * a + t] = fast_exp2(fmaf(lg[4 * a + t], sl2, -lsv[t]));
     }
     if (edge) {
 #pragma unroll
@@ -1095,6 +1102,7 @@ __global__ __launch_bounds__(NTHREADS, (kv_min_blocks<OP, D, G>())) void bwd_kv_
 
   float ucarry = 0.f;
   const float sl2 = scale * LOG2E;
+  const float neg_inv_scale = -1.f / scale;
   // query tiles the workgroup visits, last to first: NB-1 down to the first that reaches its keys
   const int qb_lo = bxy.x * NWAVES;
   const int ntiles = NB - qb_lo;
@@ -1214,18 +1222,19 @@ __global__ __launch_bounds__(NTHREADS, (kv_min_blocks<OP, D, G>())) void bwd_kv_
           for (int s = 0; s < NS; ++s) l0 = OP::mma(OP::ld_std(q0s, LDK, n, h, s), k0_frag(H0, s), l0);
           f32x16 fs;
           uint32_t gate;
-          selection_tile<true>(l0, (j < T) ? hist * LOG2E : 0.f, sl2, h, edge, mk, gate, fs);
+          selection_tile<true>(l0, (j < T) ? hist * neg_inv_scale : 0.f, h, edge, mk, gate, fs);
 
           // Per head: P and dz, dV^T += dO^T P, dK^T += Q^T dz; then g from the group's dz sum goes to
           // head 0's dK: added to head 0's own dz when the group holds it, else into dk0t.
           f32x16 dzsum, dz0;
   #pragma unroll
           for (int g = 0; g < G; ++g) {
-            f32x16 lg;
+            f32x16 lg;   // q.k - F/s
             if (H0 && g == 0) {   // head 0 itself: its logits are l0
-              lg = l0;
+  #pragma unroll
+              for (int i = 0; i < 16; ++i) lg[i] = l0[i] + fs[i];
             } else {
-              lg = zero16();
+              lg = fs;
   #pragma unroll
               for (int s = 0; s < NS; ++s) lg = OP::mma(OP::ld_std(sQ[buf][g], LDK, n, h, s), k_frag(g, s), lg);
             }
@@ -1233,7 +1242,7 @@ __global__ __launch_bounds__(NTHREADS, (kv_min_blocks<OP, D, G>())) void bwd_kv_
   #pragma unroll
             for (int s = 0; s < NS; ++s) dp = OP::mma(OP::ld_std(sdO[buf][g], LDK, n, h, s), v_frag(g, s), dp);
             f32x16 pr, dz;
-            p_dz_tile<true>(lg, dp, fs, sLse[buf][g], sDb[buf][g], sl2, h, edge, mk, pr, dz);
+            p_dz_tile<true>(lg, dp, sLse[buf][g], sDb[buf][g], sl2, h, edge, mk, pr, dz);
             acc_t(dvt[g], sdOt[buf][g], pr, split_keys);
             if (g == 0) {
               dzsum = dz;
@@ -1418,6 +1427,7 @@ __global__ __launch_bounds__(NTHREADS, (dq_min_blocks<OP, D>())) void bwd_dq_ker
   for (int db = 0; db < DB; ++db) dq0acc[db] = zero16();
 
   const float sl2 = scale * LOG2E;
+  const float neg_inv_scale = -1.f / scale;
 
   // Staging of one key tile: K, V, K^T of the group (+ head 0's K, K^T).
   RowTile<elem, D> nK[NH], nV[G];
@@ -1529,16 +1539,17 @@ __global__ __launch_bounds__(NTHREADS, (dq_min_blocks<OP, D>())) void bwd_dq_ker
             l0 = OP::mma(H0 ? q_frag(0, s) : q0a[s], OP::ld_std(k0s, LDK, n, h, s), l0);
           f32x16 fs;
           uint32_t gate;
-          selection_tile<false>(l0, hist * LOG2E, sl2, h, edge, mk, gate, fs);
+          selection_tile<false>(l0, hist * neg_inv_scale, h, edge, mk, gate, fs);
 
           f32x16 zsum, dz0;
   #pragma unroll
           for (int g = 0; g < G; ++g) {
-            f32x16 lg;
+            f32x16 lg;   // q.k - F/s
             if (H0 && g == 0) {   // head 0 itself: its logits are l0, its dQ waits for g
-              lg = l0;
+  #pragma unroll
+              for (int i = 0; i < 16; ++i) lg[i] = l0[i] + fs[i];
             } else {
-              lg = zero16();
+              lg = fs;
   #pragma unroll
               for (int s = 0; s < NS; ++s)
                 lg = OP::mma(q_frag(g, s), OP::ld_std(sK[buf][g], LDK, n, h, s), lg);
@@ -1548,7 +1559,7 @@ __global__ __launch_bounds__(NTHREADS, (dq_min_blocks<OP, D>())) void bwd_dq_ker
             for (int s = 0; s < NS; ++s)
               dp = OP::mma(do_frag(g, s), OP::ld_std(sV[buf][g], LDK, n, h, s), dp);
             f32x16 pr, dz;
-            p_dz_tile<false>(lg, dp, fs, sLse[wave][g], sDb[wave][g], sl2, h, edge, mk, pr, dz);
+            p_dz_tile<false>(lg, dp, sLse[wave][g], sDb[wave][g], sl2, h, edge, mk, pr, dz);
             if (g == 0) {
               zsum = dz;
             } else {
