@@ -95,6 +95,7 @@ int64_t sa_forward_workspace_bytes(int64_t nseq, int64_t heads, int64_t tk, int6
  * scale: the logit scale s (the reference uses 1/sqrt(D); a caller that zero-pads D passes the
  * unpadded value). group: heads per wavefront (0 = automatic); damp_mode 0 none, 1 linear, 2 sqrt scales F of
  * query i by min(1, train_len/(i+1)) (or its square root), reference kernels.py:179-182.
+ * Limits (all entry points): one head's rows below 2 GiB (t * head_dim * element size < 2^31).
  */
 int sa_forward(const void* q, const void* k, const void* v,
                float* out, float* rmax, float* rden, float* carry,

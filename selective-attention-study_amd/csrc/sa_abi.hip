@@ -87,6 +87,7 @@ int sa_forward(const void* q, const void* k, const void* v, float* out, float* r
   if (!(scale > 0.f) || !(scale < INFINITY)) return SA_ERR_ARGUMENT;
   if (dtype != SA_DTYPE_BF16 && dtype != SA_DTYPE_F32) return SA_ERR_DTYPE;
   if (head_dim != 32 && head_dim != 64 && head_dim != 128) return SA_ERR_HEAD_DIM;
+  if (!rows_fit(tk, head_dim, dtype)) return SA_ERR_ARGUMENT;
   if (workspace_bytes < sa_forward_workspace_bytes(nseq, heads, tk, head_dim, dtype)) return SA_ERR_WORKSPACE;
   const FwdCall c{q,         k,     v,       out,          rmax,        rden,     carry,
                   state_in,  state_out,    state_ld,     workspace,   (int)nseq, (int)heads, (int)tq,
@@ -112,6 +113,7 @@ int sa_backward(const void* q, const void* k, const void* v, const float* out, c
   if (dtype != SA_DTYPE_BF16 && dtype != SA_DTYPE_F32) return SA_ERR_DTYPE;
   if (grad_dtype != SA_DTYPE_BF16 && grad_dtype != SA_DTYPE_F32) return SA_ERR_DTYPE;
   if (head_dim != 32 && head_dim != 64 && head_dim != 128) return SA_ERR_HEAD_DIM;
+  if (!rows_fit(t, head_dim, dtype)) return SA_ERR_ARGUMENT;
   if (group < 0 || workspace_bytes < sa_backward_workspace_bytes(nseq, heads, t, head_dim, dtype, group))
     return SA_ERR_WORKSPACE;
   const BwdCall c{q,  k,  v,  out, dout, rmax, rden, carry, dq, dk, dv, workspace, (int)nseq, (int)heads, (int)t,
@@ -132,6 +134,7 @@ int sa_decode(const void* q, const void* k, const void* v, float* out, float* se
   if (!(scale > 0.f) || !(scale < INFINITY)) return SA_ERR_ARGUMENT;
   if (dtype != SA_DTYPE_BF16 && dtype != SA_DTYPE_F32) return SA_ERR_DTYPE;
   if (head_dim != 32 && head_dim != 64 && head_dim != 128) return SA_ERR_HEAD_DIM;
+  if (!rows_fit(t, head_dim, dtype)) return SA_ERR_ARGUMENT;
   if (kv_stride == 0) kv_stride = t * head_dim;
   if (kv_stride < t * head_dim || kv_stride % 8 != 0) return SA_ERR_ARGUMENT;
   if (workspace_bytes < sa_decode_workspace_bytes(nseq, heads, t, head_dim)) return SA_ERR_WORKSPACE;

@@ -82,6 +82,25 @@ __device__ __forceinline__ Halves halves(float x) {
 
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
+// Word 3 of a raw buffer resource on gfx950 (32-bit data format; offsets in bytes, range-checked
+// against the resource's byte count: loads past it return zero).
+constexpr int RSRC_WORD3 = 0x00020000;
+
+// Element i = s[crow(i, h)]: a C-layout tile whose rows take the values of a 32-entry LDS row
+// vector (four 16-byte reads).
+__device__ __forceinline__ f32x16 rows16(const float* s, int h) {
+  f32x16 r;
+#pragma unroll
+  for (int a = 0; a < 4; ++a) {
+    const float4 v = *reinterpret_cast<const float4*>(s + 8 * a + 4 * h);
+    r[4 * a] = v.x;
+    r[4 * a + 1] = v.y;
+    r[4 * a + 2] = v.z;
+    r[4 * a + 3] = v.w;
+  }
+  return r;
+}
+
 // The wavefront index within the workgroup, as a value the compiler knows is uniform across the
 // wavefront (threadIdx.x / 64 is, but divergence analysis cannot see it): tile flags derived from
 // it become scalar branches instead of per-lane exec masks.
@@ -287,8 +306,10 @@ __device__ __forceinline__ int swz64(int r, int c) { return r * 64 + (((c + (r >
 // (each thread owns PER 16-byte chunks), store() later writes them to LDS, so the loads of the next
 // tile are in flight while the current one is computed.
 
-// [32 rows][COLS] of a row-major global matrix (row stride gld); rows >= nrows read as zero. The
-// row index is clamped and the value zeroed by select, so the load has no branch.
+// [32 rows][COLS] of a row-major global matrix (row stride gld); rows >= nrows read as zero: the
+// loads go through a buffer resource over the nrows rows (nrows * gld elements below 2 GiB, checked
+// by the host), so there is no bound check and the offsets are 32-bit (the lane's own part fixed,
+// the tile's in a scalar register).
 template <typename E, int COLS>
 struct RowTile {
   static constexpr int EPC = 16 / sizeof(E);
@@ -297,14 +318,16 @@ struct RowTile {
   static constexpr int PER = (NCH + NTHREADS - 1) / NTHREADS;
   uint4 v[PER];
   __device__ __forceinline__ void load(const E* g, int64_t gld, int row0, int nrows, int tid) {
+    const int ld = (int)gld;
+    const __amdgpu_buffer_rsrc_t rs =
+        __builtin_amdgcn_make_buffer_rsrc((void*)g, 0, nrows * ld * (int)sizeof(E), RSRC_WORD3);
 #pragma unroll
     for (int p = 0; p < PER; ++p) {
       const int c = (tid + p * NTHREADS) % NCH;   // PER * NTHREADS > NCH only for small tiles
       const int r = c / CPR, cc = (c % CPR) * EPC;
-      const int rr = min(row0 + r, nrows - 1);
-      const uint4 x = *reinterpret_cast<const uint4*>(g + (int64_t)rr * gld + cc);
-      const bool ok = row0 + r < nrows;
-      v[p] = make_uint4(ok ? x.x : 0u, ok ? x.y : 0u, ok ? x.z : 0u, ok ? x.w : 0u);
+      const auto x = __builtin_amdgcn_raw_buffer_load_b128(rs, (r * ld + cc) * (int)sizeof(E),
+                                                           row0 * ld * (int)sizeof(E), 0);
+      v[p] = make_uint4(x[0], x[1], x[2], x[3]);
     }
   }
   template <int SLD>
@@ -923,26 +946,23 @@ __device__ __forceinline__ float gpath_tile(const f32x16& z, float u_in, uint32_
   return -nrun;
 }
 
-// P = exp2(s log2e lg - lse) and dz = P (dp - dbar) on a tile, lg = q.k - F/s; lse and dbar of the
-// tile's rows come from LDS (4 consecutive rows per float4). Pairs outside j <= r, j < T are zeroed
-// on `edge` tiles (every tile when ALWAYS).
+// P = exp2(s log2e lg - lse) and dz = P dpb on a tile, lg = q.k - F/s, dpb = dO.v - dbar (the
+// product accumulated onto -dbar); lse of the tile's rows comes from LDS (4 consecutive rows per
+// float4). Pairs outside j <= r, j < T are zeroed on `edge` tiles (every tile when ALWAYS).
 template <bool ALWAYS>
-__device__ __forceinline__ void p_dz_tile(const f32x16& lg, const f32x16& dp, const float* slse,
-                                          const float* sdb, float sl2, int h, bool edge, const TileMasks& mk,
-                                          f32x16& pr, f32x16& dz) {
+__device__ __forceinline__ void p_dz_tile(const f32x16& lg, const f32x16& dpb, const float* slse, float sl2,
+                                          int h, bool edge, const TileMasks& mk, f32x16& pr, f32x16& dz) {
   if constexpr (ALWAYS) {
 #pragma unroll
     for (int a = 0; a < 4; ++a) {
       const float4 ls = *reinterpret_cast<const float4*>(slse + 8 * a + 4 * h);
-      const float4 dbv = *reinterpret_cast<const float4*>(sdb + 8 * a + 4 * h);
       const float lsv[4] = {ls.x, ls.y, ls.z, ls.w};
-      const float dbs[4] = {dbv.x, dbv.y, dbv.z, dbv.w};
 #pragma unroll
       for (int t = 0; t < 4; ++t) {
         const int i = 4 * a + t;
         const float p = fast_exp2(fmaf(lg[i], sl2, -lsv[t]));
         pr[i] = crow(i, 0) >= mk.thr_p ? p : 0.f;
-        dz[i] = pr[i] * (dp[i] - dbs[t]);
+        dz[i] = pr[i] * dpb[i];
       }
     }
   } else {
@@ -958,12 +978,7 @@ __device__ __forceinline__ void p_dz_tile(const f32x16& lg, const f32x16& dp, co
       for (int i = 0; i < 16; ++i) pr[i] = crow(i, 0) >= mk.thr_p ? pr[i] : 0.f;
     }
 #pragma unroll
-    for (int a = 0; a < 4; ++a) {
-      const float4 dbv = *reinterpret_cast<const float4*>(sdb + 8 * a + 4 * h);
-      const float dbs[4] = {dbv.x, dbv.y, dbv.z, dbv.w};
-#pragma unroll
-      for (int t = 0; t < 4; ++t) dz[4 * a + t] = pr[4 * a + t] * (dp[4 * a + t] - dbs[t]);
-    }
+    for (int i = 0; i < 16; ++i) dz[i] = pr[i] * dpb[i];
   }
 }
 
@@ -1124,7 +1139,7 @@ __global__ __launch_bounds__(NTHREADS, (kv_min_blocks<OP, D, G>())) void bwd_kv_
       const int rr = min(r, T - 1);
       const float lv = lse[row * T + rr], dv_ = dbar[row * T + rr];
       nLse[g] = r < T ? lv : INFINITY;   // rows past the end: P = 0
-      nDb[g] = r < T ? dv_ : 0.f;
+      nDb[g] = r < T ? -dv_ : 0.f;   // negated: the dO.v product accumulates onto it
     }
     if (!has_h0) {
       nQ[G].load(q + seq_row * T * D, D, qbase, T, tid);
@@ -1238,11 +1253,11 @@ __global__ __launch_bounds__(NTHREADS, (kv_min_blocks<OP, D, G>())) void bwd_kv_
   #pragma unroll
               for (int s = 0; s < NS; ++s) lg = OP::mma(OP::ld_std(sQ[buf][g], LDK, n, h, s), k_frag(g, s), lg);
             }
-            f32x16 dp = zero16();
+            f32x16 dp = rows16(sDb[buf][g], h);   // dO.v - dbar
   #pragma unroll
             for (int s = 0; s < NS; ++s) dp = OP::mma(OP::ld_std(sdO[buf][g], LDK, n, h, s), v_frag(g, s), dp);
             f32x16 pr, dz;
-            p_dz_tile<true>(lg, dp, sLse[buf][g], sDb[buf][g], sl2, h, edge, mk, pr, dz);
+            p_dz_tile<true>(lg, dp, sLse[buf][g], sl2, h, edge, mk, pr, dz);
             acc_t(dvt[g], sdOt[buf][g], pr, split_keys);
             if (g == 0) {
               dzsum = dz;
@@ -1410,7 +1425,7 @@ __global__ __launch_bounds__(NTHREADS, (dq_min_blocks<OP, D>())) void bwd_dq_ker
     if (lane < TILE) {
       const int r = qbase + lane;
       sLse[wave][g][lane] = (r < T) ? lse[row * T + r] : INFINITY;   // rows past the end: P = 0
-      sDb[wave][g][lane] = (r < T) ? dbar[row * T + r] : 0.f;
+      sDb[wave][g][lane] = (r < T) ? -dbar[row * T + r] : 0.f;   // negated: dO.v accumulates onto it
     }
   }
   if (!has_h0) {
@@ -1554,12 +1569,12 @@ __global__ __launch_bounds__(NTHREADS, (dq_min_blocks<OP, D>())) void bwd_dq_ker
               for (int s = 0; s < NS; ++s)
                 lg = OP::mma(q_frag(g, s), OP::ld_std(sK[buf][g], LDK, n, h, s), lg);
             }
-            f32x16 dp = zero16();
+            f32x16 dp = rows16(sDb[wave][g], h);   // dO.v - dbar
   #pragma unroll
             for (int s = 0; s < NS; ++s)
               dp = OP::mma(do_frag(g, s), OP::ld_std(sV[buf][g], LDK, n, h, s), dp);
             f32x16 pr, dz;
-            p_dz_tile<false>(lg, dp, sLse[wave][g], sDb[wave][g], sl2, h, edge, mk, pr, dz);
+            p_dz_tile<false>(lg, dp, sLse[wave][g], sl2, h, edge, mk, pr, dz);
             if (g == 0) {
               zsum = dz;
             } else {
@@ -1667,9 +1682,7 @@ __global__ __launch_bounds__(NTHREADS) void bwd_finish_kernel(
 #ifndef SA_DEC_NR
 #define SA_DEC_NR 8
 #endif
-// Word 3 of a raw buffer resource on gfx950 (32-bit data format; offsets in bytes, range-checked
-// against the resource's byte count: loads past it return zero).
-constexpr int DEC_RSRC_WORD3 = 0x00020000;
+
 #ifndef SA_DEC_MINB
 #define SA_DEC_MINB 1
 #endif
@@ -1740,9 +1753,9 @@ __global__ __launch_bounds__(NTHREADS, SA_DEC_MINB) void decode_partial_kernel(
   // buffer resources over the head's t cached rows: the loads take one lane offset (row slot and
   // column slice) plus a wavefront-uniform offset of the rows, and rows at or past t read as zero
   constexpr int RB = D * (int)sizeof(E);   // bytes per cached row
-  const int nbytes = t * RB;               // < 2^31, checked by the host
-  const __amdgpu_buffer_rsrc_t krs = __builtin_amdgcn_make_buffer_rsrc((void*)(k + row * kvs), 0, nbytes, DEC_RSRC_WORD3);
-  const __amdgpu_buffer_rsrc_t vrs = __builtin_amdgcn_make_buffer_rsrc((void*)(v + row * kvs), 0, nbytes, DEC_RSRC_WORD3);
+  const int nbytes = t * RB;               // < 2^31 (rows_fit, checked by the C ABI)
+  const __amdgpu_buffer_rsrc_t krs = __builtin_amdgcn_make_buffer_rsrc((void*)(k + row * kvs), 0, nbytes, RSRC_WORD3);
+  const __amdgpu_buffer_rsrc_t vrs = __builtin_amdgcn_make_buffer_rsrc((void*)(v + row * kvs), 0, nbytes, RSRC_WORD3);
   const int loff = kq * RB + EPC * dc * (int)sizeof(E);
   float m = -INFINITY, l = 0.f, o[EPC];
 #pragma unroll
@@ -2114,8 +2127,7 @@ int decode_impl(const DecCall& c) {
   const int64_t rows = (int64_t)c.nseq * c.heads;
   const int chunk = decode_chunk(rows, c.t);
   const int nchunk = (int)cdiv(c.t, chunk);
-  if (nchunk > DEC_FIN_MAXPARTS || (int64_t)c.t * D * (int64_t)sizeof(elem) >= ((int64_t)1 << 31))
-    return SA_ERR_ARGUMENT;
+  if (nchunk > DEC_FIN_MAXPARTS) return SA_ERR_ARGUMENT;
   // workspace: maxima, sums (rows * nchunk each, padded to 4) and outputs (rows * nchunk * D) of the
   // partials, then the updated selection rows
   const int64_t np = align_up(rows * nchunk, 4);
