@@ -126,10 +126,10 @@ inline bool valid_dims(int64_t nseq, int64_t heads, int64_t t) {
   return nseq >= 1 && heads >= 1 && t >= 1 && nseq < 65536 && heads < 65536 && t < lim && nseq * heads < 65536;
 }
 
-// The kernels read one head's rows through buffer resources with 32-bit byte offsets: t rows of
-// head_dim elements must stay below 2 GiB.
+// The kernels read one head's rows (and its transposed copies, rows padded to a multiple of 64)
+// through buffer resources with 32-bit byte offsets: they must stay below 2 GiB.
 inline bool rows_fit(int64_t t, int64_t head_dim, int dtype) {
-  return t * head_dim * (dtype == SA_DTYPE_BF16 ? 2 : 4) < ((int64_t)1 << 31);
+  return (t + 64) * head_dim * (dtype == SA_DTYPE_BF16 ? 2 : 4) < ((int64_t)1 << 31);
 }
 
 

@@ -344,7 +344,7 @@ struct RowTile {
 
 // Columns col0..col0+31 of ROWS rows of one of this library's transposed copies: row stride gld,
 // a multiple of 64 elements, zero-filled past the sequence, so every 16-byte chunk is in bounds and
-// the load needs no check.
+// the load needs no check. Buffer loads as for RowTile: 32-bit offsets, the lane's part fixed.
 template <typename E, int ROWS>
 struct ColTile {
   static constexpr int EPC = 16 / sizeof(E);
@@ -353,11 +353,16 @@ struct ColTile {
   static constexpr int PER = (NCH + NTHREADS - 1) / NTHREADS;
   uint4 v[PER];
   __device__ __forceinline__ void load(const E* g, int64_t gld, int col0, int tid) {
+    const int ld = (int)gld;
+    const __amdgpu_buffer_rsrc_t rs =
+        __builtin_amdgcn_make_buffer_rsrc((void*)g, 0, ROWS * ld * (int)sizeof(E), RSRC_WORD3);
 #pragma unroll
     for (int p = 0; p < PER; ++p) {
       const int c = (tid + p * NTHREADS) % NCH;
       const int r = c / CPR, cc = (c % CPR) * EPC;
-      v[p] = *reinterpret_cast<const uint4*>(g + (int64_t)r * gld + col0 + cc);
+      const auto x = __builtin_amdgcn_raw_buffer_load_b128(rs, (r * ld + cc) * (int)sizeof(E),
+                                                           col0 * (int)sizeof(E), 0);
+      v[p] = make_uint4(x[0], x[1], x[2], x[3]);
     }
   }
   template <int SLD>
