@@ -1242,7 +1242,7 @@ __global__ __launch_bounds__(NTHREADS, (kv_min_blocks<OP, D, G>())) void bwd_kv_
           for (int s = 0; s < NS; ++s) l0 = OP::mma(OP::ld_std(q0s, LDK, n, h, s), k0_frag(H0, s), l0);
           f32x16 fs;
           uint32_t gate;
-          selection_tile<true>(l0, (j < T) ? hist * neg_inv_scale : 0.f, h, edge, mk, gate, fs);
+          selection_tile<false>(l0, (j < T) ? hist * neg_inv_scale : 0.f, h, edge, mk, gate, fs);
 
           // Per head: P and dz, dV^T += dO^T P, dK^T += Q^T dz; then g from the group's dz sum goes to
           // head 0's dK: added to head 0's own dz when the group holds it, else into dk0t.
@@ -1262,7 +1262,7 @@ __global__ __launch_bounds__(NTHREADS, (kv_min_blocks<OP, D, G>())) void bwd_kv_
   #pragma unroll
             for (int s = 0; s < NS; ++s) dp = OP::mma(OP::ld_std(sdO[buf][g], LDK, n, h, s), v_frag(g, s), dp);
             f32x16 pr, dz;
-            p_dz_tile<true>(lg, dp, sLse[buf][g], sl2, h, edge, mk, pr, dz);
+            p_dz_tile<false>(lg, dp, sLse[buf][g], sl2, h, edge, mk, pr, dz);
             acc_t(dvt[g], sdOt[buf][g], pr, split_keys);
             if (g == 0) {
               dzsum = dz;
