@@ -65,8 +65,11 @@ inline int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
 
 inline int launch_status() { return hipGetLastError() == hipSuccess ? SA_OK : SA_ERR_LAUNCH; }
 
+// Heads per wavefront of the forward (a group shares head 0's selection work: its logits, F):
+// 4 at head dim <= 32, 2 at 64 (two heads' output sums in registers leave two workgroups per CU,
+// which measures faster than three with one head), 1 beyond; fp32 storage 1.
 #ifndef SA_FWD_GROUP_D64
-#define SA_FWD_GROUP_D64 1
+#define SA_FWD_GROUP_D64 2
 #endif
 inline int auto_group(int dtype, int64_t D, int64_t heads, int requested, bool backward) {
   int g = requested;

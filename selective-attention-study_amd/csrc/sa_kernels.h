@@ -512,6 +512,9 @@ __global__ __launch_bounds__(NTHREADS) void sel_scan_kernel(
 
 // Workgroups per CU the forward's register allocation must allow: three at bf16 head dims <= 64
 // (its LDS fits three), which holds it to 168 registers without spills.
+#ifndef SA_FWD_NBUF
+#define SA_FWD_NBUF 2   // LDS buffers of the key tiles (2: the next tile is written while one is read)
+#endif
 #ifndef SA_FWD_MIN_BLOCKS
 #define SA_FWD_MIN_BLOCKS 3
 #endif
@@ -534,7 +537,7 @@ __global__ __launch_bounds__(NTHREADS, (fwd_min_blocks<OP, D, G>())) void fwd_ke
   constexpr int AS = OP::acc_steps;
   constexpr int NH = G + 1;
   constexpr int TILE_BYTES = (NH * TILE * LDK + G * D * LDV) * (int)sizeof(elem);
-  constexpr int NBUF = 2 * TILE_BYTES <= 120 * 1024 ? 2 : 1;
+  constexpr int NBUF = (SA_FWD_NBUF >= 2 && 2 * TILE_BYTES <= 120 * 1024) ? 2 : 1;
 
   __shared__ __attribute__((aligned(16))) elem sK[NBUF][NH][TILE * LDK];
   __shared__ __attribute__((aligned(16))) elem sVt[NBUF][G][D * LDV];
@@ -866,6 +869,9 @@ __global__ __launch_bounds__(NTHREADS) void fill_zero_kernel(float4* __restrict_
 
 #ifndef SA_DQ_PIPE
 #define SA_DQ_PIPE 0
+#endif
+#ifndef SA_DQ_NBUF
+#define SA_DQ_NBUF 2
 #endif
 #ifndef SA_DQ_MIN_BLOCKS
 #define SA_DQ_MIN_BLOCKS 2
@@ -1348,7 +1354,7 @@ __global__ __launch_bounds__(NTHREADS, (dq_min_blocks<OP, D>())) void bwd_dq_ker
   constexpr int NH = G + 1;
   constexpr bool DQ_PIPE = SA_DQ_PIPE != 0;
   constexpr int TILE_BYTES = (NH * (TILE * LDK + D * LDKT) + G * TILE * LDK) * (int)sizeof(elem);
-  constexpr int NBUF = (DQ_PIPE && 2 * TILE_BYTES <= 120 * 1024) ? 2 : 1;
+  constexpr int NBUF = (DQ_PIPE && SA_DQ_NBUF >= 2 && 2 * TILE_BYTES <= 120 * 1024) ? 2 : 1;
 
   __shared__ __attribute__((aligned(16))) elem sK[NBUF][NH][TILE * LDK];
   __shared__ __attribute__((aligned(16))) elem sKt[NBUF][NH][D * LDKT];
