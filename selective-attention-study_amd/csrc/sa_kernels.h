@@ -86,6 +86,53 @@ __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_ex
 // against the resource's byte count: loads past it return zero).
 constexpr int RSRC_WORD3 = 0x00020000;
 
+// A 32 x 32 bf16 tile kept transposed in LDS for the transposing read ds_read_b64_tr_b16: rows of
+// 32 elements (64 bytes), the 8-byte chunk c of row r stored at chunk c ^ ((r / 4) mod 8). The
+// read gives lane i of each 16-lane group, element t, the element i % 4 of the 8 bytes that lane
+// 4t + i/4 of the group addresses (measured on gfx950). A lane-per-row write of one chunk from 32
+// rows, and a transposing read of four consecutive rows, then each touch every bank once.
+__device__ __forceinline__ int trt_off(int r, int c) { return r * 32 + ((c ^ ((r >> 2) & 7)) << 2); }
+
+typedef short short4v __attribute__((ext_vector_type(4)));
+
+// Writes a C-layout tile x (lane = column n, element i = row crow(i, h)) transposed: row n of the
+// LDS tile holds column n of x, 4 consecutive rows of x per 8-byte write. LO: the rounding
+// residuals x - bf16(x) instead.
+template <bool LO>
+__device__ __forceinline__ void put_tr(uint16_t* t, const f32x16& x, int n, int h) {
+#pragma unroll
+  for (int a = 0; a < 4; ++a) {
+    typedef bf16_t bf16x4 __attribute__((__vector_size__(4 * sizeof(bf16_t))));
+    bf16x4 v;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const float f = x[4 * a + e];
+      v[e] = LO ? (bf16_t)(f - (float)(bf16_t)f) : (bf16_t)f;
+    }
+    *reinterpret_cast<bf16x4*>(t + trt_off(n, 2 * a + h)) = v;
+  }
+}
+
+// The A (or B) operand of K step s read from such a tile: lane l gets row l % 32 of the
+// untransposed tile, elements 16s + 8(l / 32) + 0..7, in order.
+__device__ __forceinline__ bf16x8 get_tr(const uint16_t* t, int lane, int s) {
+  const int g = lane >> 4, k = lane & 15;
+  const int n0 = 16 * (g & 1), hh = g >> 1;
+  bf16x8 f;
+#pragma unroll
+  for (int hf = 0; hf < 2; ++hf) {
+    const int r = 16 * s + 8 * hh + 4 * hf + (k >> 2);
+    typedef __attribute__((address_space(3))) short4v* lds_s4;
+    const short4v v = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s4)(t + trt_off(r, (n0 >> 2) + (k & 3))));
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const short x = v[e];
+      f[4 * hf + e] = *reinterpret_cast<const bf16_t*>(&x);
+    }
+  }
+  return f;
+}
+
 // Element i = s[crow(i, h)]: a C-layout tile whose rows take the values of a 32-entry LDS row
 // vector (four 16-byte reads).
 __device__ __forceinline__ f32x16 rows16(const float* s, int h) {
@@ -1490,6 +1537,31 @@ __global__ __launch_bounds__(NTHREADS, (dq_min_blocks<OP, D>())) void bwd_dq_ker
   // takes a second pass.
   auto acc_xk = [&](f32x16 (&acc)[DB], const f32x16& x, const elem* ktile, bool split) {
     frag zf[AS];
+    if constexpr (sizeof(elem) == 2) {
+      // bf16: X goes to the tile transposed (4 rows per write) and comes back through the
+      // transposing read
+      put_tr<false>(zs, x, n, h);
+      lds_wave_sync();
+#pragma unroll
+      for (int s = 0; s < AS; ++s) zf[s] = get_tr(zs, lane, s);
+#pragma unroll
+      for (int db = 0; db < DB; ++db)
+#pragma unroll
+        for (int s = 0; s < AS; ++s) acc[db] = OP::mma(zf[s], OP::ld_std(ktile, LDKT, db * 32 + n, h, s), acc[db]);
+      if (split) {
+        lds_wave_sync();
+        put_tr<true>(zs, x, n, h);
+        lds_wave_sync();
+#pragma unroll
+        for (int s = 0; s < AS; ++s) zf[s] = get_tr(zs, lane, s);
+#pragma unroll
+        for (int db = 0; db < DB; ++db)
+#pragma unroll
+          for (int s = 0; s < AS; ++s) acc[db] = OP::mma(zf[s], OP::ld_std(ktile, LDKT, db * 32 + n, h, s), acc[db]);
+      }
+      lds_wave_sync();
+      return;
+    }
 #pragma unroll
     for (int i = 0; i < 16; ++i) zs[crow(i, h) * LDZ + n] = OP::to_elem(x[i]);
     lds_wave_sync();
