@@ -34,7 +34,8 @@
 //   A (32xK) / B (Kx32):         lane l holds row (A) / column (B) l%32 and K elements
 //                                [KS*step + (KS/2)*h, +KS/2) with KS = 16 (bf16) or 2 (fp32).
 // A C-layout tile fed back as a B operand keeps its registers in place; the matching A operand
-// is then read with the C layout's row order (ld_perm).
+// is then read with the C layout's row order (ld_perm; bf16 tiles read that way are staged with
+// their columns in that order, ColTile::store_crow, so a fragment is one 16-byte read).
 
 
 #pragma once
@@ -166,7 +167,8 @@ struct OpBF16 {
   typedef bf16x8 frag;
   static constexpr int KS = 16;
   static constexpr int KPAD = 8;     // LDS row padding (elements) of [rows][D] tiles
-  static constexpr int TPAD = 4;     // LDS row padding (elements) of [rows][32] tiles
+  static constexpr int TPAD = 8;     // LDS row padding (elements) of [rows][32] tiles: 80-byte rows,
+                                     // 16-byte aligned, distinct banks for 16 rows
 
   static __device__ __forceinline__ f32x16 mma(frag a, frag b, f32x16 c) {
     return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
@@ -181,13 +183,10 @@ struct OpBF16 {
   static __device__ __forceinline__ frag ld_std(const elem* p, int64_t ld, int r, int h, int s) {
     return *reinterpret_cast<const frag*>(p + r * ld + s * 16 + 8 * h);
   }
-  // Row r, K elements in C-layout row order for step s: [16s+4h, +4) and [16s+8+4h, +4).
+  // Row r, K elements in C-layout row order for step s -- columns [16s+4h, +4) and [16s+8+4h, +4)
+  // -- from a tile whose columns were stored in that order (ColTile::store_crow): one 16-byte read.
   static __device__ __forceinline__ frag ld_perm(const elem* p, int64_t ld, int r, int h, int s) {
-    const elem* base = p + r * ld + s * 16 + 4 * h;
-    uint2 lo = *reinterpret_cast<const uint2*>(base);
-    uint2 hi = *reinterpret_cast<const uint2*>(base + 8);
-    uint4 u = make_uint4(lo.x, lo.y, hi.x, hi.y);
-    return *reinterpret_cast<frag*>(&u);
+    return *reinterpret_cast<const frag*>(p + r * ld + s * 16 + 8 * h);
   }
   // C-layout registers [8s, 8s+8) as an operand (round to nearest even).
   static __device__ __forceinline__ frag from_acc(const f32x16& c, int s) {
@@ -234,7 +233,7 @@ struct OpF32 {
     return p[r * ld + 2 * s + h];
   }
   static __device__ __forceinline__ frag ld_perm(const elem* p, int64_t ld, int r, int h, int s) {
-    return p[r * ld + crow(s, h)];
+    return p[r * ld + crow(s, h)];   // a standard-order tile (ColTile::store_crow stores fp32 as is)
   }
   static __device__ __forceinline__ frag from_acc(const f32x16& c, int s) { return c[s]; }
   static constexpr bool SPLIT = false;   // fp32 operands are exact already
@@ -429,6 +428,29 @@ struct ColTile {
         u.q = v[p];
 #pragma unroll
         for (int e = 0; e < EPC; ++e) dst[e] = u.e[e];
+      }
+    }
+  }
+  // bf16: the columns of each 16-column block in C-layout row order -- groups of four columns
+  // 0, 2, 1, 3 -- so OpBF16::ld_perm reads a fragment with one 16-byte read; fp32 as store().
+  template <int SLD>
+  __device__ __forceinline__ void store_crow(E* s, int tid) const {
+    if constexpr (sizeof(E) != 2) {
+      store<SLD>(s, tid);
+    } else {
+      static_assert((SLD * 2) % 16 == 0, "C-layout-order tiles need 16-byte row alignment");
+#pragma unroll
+      for (int p = 0; p < PER; ++p) {
+        const int c = tid + p * NTHREADS;
+        const int r = (c % NCH) / CPR, cc = (c % CPR) * EPC;
+        if (!(NCH % NTHREADS == 0 || c < NCH)) continue;
+        // cc is a multiple of 8: its groups of four are 2(cc%16)/8 and that + 1, at 0 -> 0, 1 -> 2,
+        // 2 -> 1, 3 -> 3
+        const int a0 = (cc & 15) >> 2;
+        const int a1 = a0 + 1;
+        E* row = s + r * SLD + (cc & ~15);
+        reinterpret_cast<uint2*>(row + 4 * (((a0 & 1) << 1) | (a0 >> 1)))[0] = make_uint2(v[p].x, v[p].y);
+        reinterpret_cast<uint2*>(row + 4 * (((a1 & 1) << 1) | (a1 >> 1)))[0] = make_uint2(v[p].z, v[p].w);
       }
     }
   }
@@ -673,7 +695,7 @@ __global__ __launch_bounds__(NTHREADS, (fwd_min_blocks<OP, D, G>())) void fwd_ke
 #pragma unroll
     for (int g = 0; g < G; ++g) {
       nK[g].template store<LDK>(sK[buf][g], tid);
-      nVt[g].template store<LDV>(sVt[buf][g], tid);
+      nVt[g].template store_crow<LDV>(sVt[buf][g], tid);
     }
     if (!has_h0) nK[G].template store<LDK>(sK[buf][G], tid);
     if (tid < NWAVES * TILE) sC[buf][tid >> 5][tid & (TILE - 1)] = nC;
@@ -1208,9 +1230,9 @@ __global__ __launch_bounds__(NTHREADS, (kv_min_blocks<OP, D, G>())) void bwd_kv_
 #pragma unroll
     for (int g = 0; g < G; ++g) {
       nQ[g].template store<LDK>(sQ[buf][g], tid);
-      nQt[g].template store<LDV>(sQt[buf][g], tid);
+      nQt[g].template store_crow<LDV>(sQt[buf][g], tid);
       ndO[g].template store<LDK>(sdO[buf][g], tid);
-      ndOt[g].template store<LDV>(sdOt[buf][g], tid);
+      ndOt[g].template store_crow<LDV>(sdOt[buf][g], tid);
       if (tid < TILE) {
         sLse[buf][g][tid] = nLse[g];
         sDb[buf][g][tid] = nDb[g];
@@ -1218,7 +1240,7 @@ __global__ __launch_bounds__(NTHREADS, (kv_min_blocks<OP, D, G>())) void bwd_kv_
     }
     if (!has_h0) {
       nQ[G].template store<LDK>(sQ[buf][G], tid);
-      nQt[G].template store<LDV>(sQt[buf][G], tid);
+      nQt[G].template store_crow<LDV>(sQt[buf][G], tid);
     }
   };
 
