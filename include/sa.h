@@ -95,7 +95,8 @@ int64_t sa_forward_workspace_bytes(int64_t nseq, int64_t heads, int64_t tk, int6
  * scale: the logit scale s (the reference uses 1/sqrt(D); a caller that zero-pads D passes the
  * unpadded value). group: heads per wavefront (0 = automatic); damp_mode 0 none, 1 linear, 2 sqrt scales F of
  * query i by min(1, train_len/(i+1)) (or its square root), reference kernels.py:179-182.
- * Limits (all entry points): one head's rows below 2 GiB (t * head_dim * element size < 2^31).
+ * Limits (all entry points): one head's rows below 2 GiB ((t + 64) * row stride * element size
+ * < 2^31; the row stride is head_dim here).
  */
 int sa_forward(const void* q, const void* k, const void* v,
                float* out, float* rmax, float* rden, float* carry,
@@ -104,6 +105,36 @@ int sa_forward(const void* q, const void* k, const void* v,
                int64_t nseq, int64_t heads, int64_t tq, int64_t tk, int64_t q_offset,
                int64_t kv_stride, int64_t head_dim, float scale, int dtype, int exempt, int group,
                int damp_mode, int64_t train_len, void* stream);
+
+/*
+ * Element strides of a view of a (nseq, heads, rows, head_dim) tensor whose head_dim elements per
+ * row are contiguous: element (b, h, r, d) sits at p + b * seq + h * head + r * row + d.
+ * Strides are multiples of 8 (bf16) or 4 (fp32) elements, row >= head_dim.
+ */
+typedef struct sa_view_strides {
+  int64_t seq, head, row;
+} sa_view_strides;
+
+/*
+ * sa_forward on views: q, k and v may be any (sequence, head, row) views, e.g. slices of one
+ * packed projection (B, T, 3, heads, head_dim) read in place -- the split and transpose of the
+ * reference's model (model.py:59-67) then cost nothing. y (may be NULL) receives the output
+ * again, in the storage dtype, through its own view (e.g. (B, T, heads, head_dim), the layout
+ * the output projection reads, mixers.py:94's cast included); `out` stays the fp32
+ * (nseq, heads, tq, head_dim) output the backward needs. Layer-boundary fusion; no reference
+ * counterpart (the reference copies). kv_stride of sa_forward corresponds to
+ * k_strides = v_strides = {heads * kv_stride, kv_stride, head_dim}. Pointers 16-byte aligned.
+ */
+int sa_forward_strided(const void* q, const sa_view_strides* q_strides,
+                       const void* k, const sa_view_strides* k_strides,
+                       const void* v, const sa_view_strides* v_strides,
+                       float* out, void* y, const sa_view_strides* y_strides,
+                       float* rmax, float* rden, float* carry,
+                       const float* state_in, float* state_out, int64_t state_ld,
+                       void* workspace, int64_t workspace_bytes,
+                       int64_t nseq, int64_t heads, int64_t tq, int64_t tk, int64_t q_offset,
+                       int64_t head_dim, float scale, int dtype, int exempt, int group,
+                       int damp_mode, int64_t train_len, void* stream);
 
 /* Bytes of scratch sa_backward needs for the same `group` argument (-1 for invalid sizes). */
 int64_t sa_backward_workspace_bytes(int64_t nseq, int64_t heads, int64_t t, int64_t head_dim, int dtype, int group);
@@ -126,6 +157,24 @@ int sa_backward(const void* q, const void* k, const void* v, const float* out, c
                 void* workspace, int64_t workspace_bytes,
                 int64_t nseq, int64_t heads, int64_t t, int64_t head_dim, float scale, int dtype,
                 int grad_dtype, int exempt, int group, void* stream);
+
+/*
+ * sa_backward on views: q, k, v and dout read through their views, dq, dk, dv written through
+ * theirs (e.g. straight into the gradient of a packed (B, T, 3, heads, head_dim) projection, so
+ * no gradient is assembled from slices). `out` is sa_forward(_strided)'s fp32 output.
+ * Layer-boundary fusion; no reference counterpart (reference kernels.py:621-666 copies).
+ */
+int sa_backward_strided(const void* q, const sa_view_strides* q_strides,
+                        const void* k, const sa_view_strides* k_strides,
+                        const void* v, const sa_view_strides* v_strides,
+                        const float* out, const void* dout, const sa_view_strides* dout_strides,
+                        const float* rmax, const float* rden, const float* carry,
+                        void* dq, const sa_view_strides* dq_strides,
+                        void* dk, const sa_view_strides* dk_strides,
+                        void* dv, const sa_view_strides* dv_strides,
+                        void* workspace, int64_t workspace_bytes,
+                        int64_t nseq, int64_t heads, int64_t t, int64_t head_dim, float scale, int dtype,
+                        int grad_dtype, int exempt, int group, void* stream);
 
 /* Bytes of scratch sa_decode needs (per-chunk partial softmax sums, the new state rows) for t keys. */
 int64_t sa_decode_workspace_bytes(int64_t nseq, int64_t heads, int64_t t, int64_t head_dim);

@@ -21,7 +21,7 @@ using namespace sa_host;
 
 extern "C" {
 
-int sa_abi_version(void) { return 3; }
+int sa_abi_version(void) { return 4; }
 
 int sa_timing_enable(int on) {
   TimingRegistry& r = timing();
@@ -80,6 +80,35 @@ int sa_forward(const void* q, const void* k, const void* v, float* out, float* r
   if (!valid_dims(nseq, heads, tk) || tq < 1 || q_offset < 0 || q_offset + tq != tk) return SA_ERR_ARGUMENT;
   if (kv_stride == 0) kv_stride = tk * head_dim;
   if (kv_stride < tk * head_dim || kv_stride % 8 != 0) return SA_ERR_ARGUMENT;
+  if (dtype != SA_DTYPE_BF16 && dtype != SA_DTYPE_F32) return SA_ERR_DTYPE;
+  if (head_dim != 32 && head_dim != 64 && head_dim != 128) return SA_ERR_HEAD_DIM;
+  const sa_view_strides qs{heads * tq * head_dim, tq * head_dim, head_dim};
+  const sa_view_strides ks{heads * kv_stride, kv_stride, head_dim};
+  return sa_forward_strided(q, &qs, k, &ks, v, &ks, out, nullptr, nullptr, rmax, rden, carry, state_in, state_out,
+                            state_ld, workspace, workspace_bytes, nseq, heads, tq, tk, q_offset, head_dim, scale,
+                            dtype, exempt, group, damp_mode, train_len, stream);
+}
+
+// A view's strides are usable by the kernels: non-negative, 16-byte multiples (rows are read in
+// 16-byte chunks), and one head's rows (t + 64 of them, with the transposed copies' padding)
+// within the 2 GiB a buffer resource addresses.
+static bool view_ok(const sa_view_strides* s, int64_t t, int64_t head_dim, int dtype, bool output) {
+  if (!s) return false;
+  const int64_t epc = dtype == SA_DTYPE_BF16 ? 8 : 4;
+  if (s->seq < 0 || s->head < 0 || s->row < head_dim) return false;
+  if (s->seq % epc || s->head % epc || s->row % epc) return false;
+  if (output && s->head < head_dim) return false;   // distinct heads of a row must not overlap
+  return rows_fit(t, s->row, dtype);
+}
+
+int sa_forward_strided(const void* q, const sa_view_strides* q_strides, const void* k,
+                       const sa_view_strides* k_strides, const void* v, const sa_view_strides* v_strides,
+                       float* out, void* y, const sa_view_strides* y_strides, float* rmax, float* rden,
+                       float* carry, const float* state_in, float* state_out, int64_t state_ld, void* workspace,
+                       int64_t workspace_bytes, int64_t nseq, int64_t heads, int64_t tq, int64_t tk,
+                       int64_t q_offset, int64_t head_dim, float scale, int dtype, int exempt, int group,
+                       int damp_mode, int64_t train_len, void* stream) {
+  if (!valid_dims(nseq, heads, tk) || tq < 1 || q_offset < 0 || q_offset + tq != tk) return SA_ERR_ARGUMENT;
   if (!q || !k || !v || !out || !rmax || !rden || !carry || !state_out || !workspace) return SA_ERR_ARGUMENT;
   if (q_offset > 0 && !state_in) return SA_ERR_ARGUMENT;
   if (state_ld < tk || exempt < 1 || damp_mode < 0 || damp_mode > 2 || (damp_mode && train_len < 1))
@@ -87,12 +116,41 @@ int sa_forward(const void* q, const void* k, const void* v, float* out, float* r
   if (!(scale > 0.f) || !(scale < INFINITY)) return SA_ERR_ARGUMENT;
   if (dtype != SA_DTYPE_BF16 && dtype != SA_DTYPE_F32) return SA_ERR_DTYPE;
   if (head_dim != 32 && head_dim != 64 && head_dim != 128) return SA_ERR_HEAD_DIM;
-  if (!rows_fit(tk, head_dim, dtype)) return SA_ERR_ARGUMENT;
+  if (!view_ok(q_strides, tq, head_dim, dtype, false) || !view_ok(k_strides, tk, head_dim, dtype, false) ||
+      !view_ok(v_strides, tk, head_dim, dtype, false) || (y && !view_ok(y_strides, tq, head_dim, dtype, true)))
+    return SA_ERR_ARGUMENT;
+  if (((uintptr_t)q | (uintptr_t)k | (uintptr_t)v | (uintptr_t)y) % 16) return SA_ERR_ARGUMENT;
   if (workspace_bytes < sa_forward_workspace_bytes(nseq, heads, tk, head_dim, dtype)) return SA_ERR_WORKSPACE;
-  const FwdCall c{q,         k,     v,       out,          rmax,        rden,     carry,
-                  state_in,  state_out,    state_ld,     workspace,   (int)nseq, (int)heads, (int)tq,
-                  (int)tk,   kv_stride,    (int)q_offset, scale,      exempt,    group,      damp_mode,
-                  (float)train_len,        (int)head_dim, static_cast<hipStream_t>(stream)};
+  auto st = [](const sa_view_strides* p) { return p ? Strides{p->seq, p->head, (int)p->row} : Strides{0, 0, 0}; };
+  FwdCall c{};
+  c.q = q;
+  c.k = k;
+  c.v = v;
+  c.qs = st(q_strides);
+  c.ks = st(k_strides);
+  c.vs = st(v_strides);
+  c.y = y;
+  c.ys = st(y_strides);
+  c.out = out;
+  c.rmax = rmax;
+  c.rden = rden;
+  c.carry = carry;
+  c.state_in = state_in;
+  c.state_out = state_out;
+  c.state_ld = state_ld;
+  c.ws = workspace;
+  c.nseq = (int)nseq;
+  c.H = (int)heads;
+  c.Tq = (int)tq;
+  c.Tk = (int)tk;
+  c.q_off = (int)q_offset;
+  c.scale = scale;
+  c.exempt = exempt;
+  c.group = group;
+  c.damp_mode = damp_mode;
+  c.train_len = (float)train_len;
+  c.head_dim = (int)head_dim;
+  c.st = static_cast<hipStream_t>(stream);
   return dtype == SA_DTYPE_BF16 ? forward_bf16(c) : forward_f32(c);
 }
 
@@ -106,6 +164,20 @@ int sa_backward(const void* q, const void* k, const void* v, const float* out, c
                 const float* rden, const float* carry, void* dq, void* dk, void* dv, void* workspace,
                 int64_t workspace_bytes, int64_t nseq, int64_t heads, int64_t t, int64_t head_dim, float scale,
                 int dtype, int grad_dtype, int exempt, int group, void* stream) {
+  const sa_view_strides c{heads * t * head_dim, t * head_dim, head_dim};
+  return sa_backward_strided(q, &c, k, &c, v, &c, out, dout, &c, rmax, rden, carry, dq, &c, dk, &c, dv, &c,
+                             workspace, workspace_bytes, nseq, heads, t, head_dim, scale, dtype, grad_dtype, exempt,
+                             group, stream);
+}
+
+int sa_backward_strided(const void* q, const sa_view_strides* q_strides, const void* k,
+                        const sa_view_strides* k_strides, const void* v, const sa_view_strides* v_strides,
+                        const float* out, const void* dout, const sa_view_strides* dout_strides, const float* rmax,
+                        const float* rden, const float* carry, void* dq, const sa_view_strides* dq_strides, void* dk,
+                        const sa_view_strides* dk_strides, void* dv, const sa_view_strides* dv_strides,
+                        void* workspace, int64_t workspace_bytes, int64_t nseq, int64_t heads, int64_t t,
+                        int64_t head_dim, float scale, int dtype, int grad_dtype, int exempt, int group,
+                        void* stream) {
   if (!valid_dims(nseq, heads, t) || exempt < 1) return SA_ERR_ARGUMENT;
   if (!(scale > 0.f) || !(scale < INFINITY)) return SA_ERR_ARGUMENT;
   if (!q || !k || !v || !out || !dout || !rmax || !rden || !carry || !dq || !dk || !dv || !workspace)
@@ -113,11 +185,44 @@ int sa_backward(const void* q, const void* k, const void* v, const float* out, c
   if (dtype != SA_DTYPE_BF16 && dtype != SA_DTYPE_F32) return SA_ERR_DTYPE;
   if (grad_dtype != SA_DTYPE_BF16 && grad_dtype != SA_DTYPE_F32) return SA_ERR_DTYPE;
   if (head_dim != 32 && head_dim != 64 && head_dim != 128) return SA_ERR_HEAD_DIM;
-  if (!rows_fit(t, head_dim, dtype)) return SA_ERR_ARGUMENT;
+  if (!view_ok(q_strides, t, head_dim, dtype, false) || !view_ok(k_strides, t, head_dim, dtype, false) ||
+      !view_ok(v_strides, t, head_dim, dtype, false) || !view_ok(dout_strides, t, head_dim, dtype, false) ||
+      !view_ok(dq_strides, t, head_dim, grad_dtype, true) || !view_ok(dk_strides, t, head_dim, grad_dtype, true) ||
+      !view_ok(dv_strides, t, head_dim, grad_dtype, true))
+    return SA_ERR_ARGUMENT;
+  if (((uintptr_t)q | (uintptr_t)k | (uintptr_t)v | (uintptr_t)dout) % 16) return SA_ERR_ARGUMENT;
   if (group < 0 || workspace_bytes < sa_backward_workspace_bytes(nseq, heads, t, head_dim, dtype, group))
     return SA_ERR_WORKSPACE;
-  const BwdCall c{q,  k,  v,  out, dout, rmax, rden, carry, dq, dk, dv, workspace, (int)nseq, (int)heads, (int)t,
-                  scale, exempt, group, grad_dtype, (int)head_dim, static_cast<hipStream_t>(stream)};
+  auto st = [](const sa_view_strides* p) { return Strides{p->seq, p->head, (int)p->row}; };
+  BwdCall c{};
+  c.q = q;
+  c.k = k;
+  c.v = v;
+  c.qs = st(q_strides);
+  c.ks = st(k_strides);
+  c.vs = st(v_strides);
+  c.out = out;
+  c.dout = dout;
+  c.dos = st(dout_strides);
+  c.rmax = rmax;
+  c.rden = rden;
+  c.carry = carry;
+  c.dq = dq;
+  c.dk = dk;
+  c.dv = dv;
+  c.ws = workspace;
+  c.dqs = st(dq_strides);
+  c.dks = st(dk_strides);
+  c.dvs = st(dv_strides);
+  c.nseq = (int)nseq;
+  c.H = (int)heads;
+  c.T = (int)t;
+  c.scale = scale;
+  c.exempt = exempt;
+  c.group = group;
+  c.grad_dtype = grad_dtype;
+  c.head_dim = (int)head_dim;
+  c.st = static_cast<hipStream_t>(stream);
   return dtype == SA_DTYPE_BF16 ? backward_bf16(c) : backward_f32(c);
 }
 

@@ -130,22 +130,34 @@ inline bool valid_dims(int64_t nseq, int64_t heads, int64_t t) {
 }
 
 // The kernels read one head's rows (and its transposed copies, rows padded to a multiple of 64)
-// through buffer resources with 32-bit byte offsets: they must stay below 2 GiB.
-inline bool rows_fit(int64_t t, int64_t head_dim, int dtype) {
-  return (t + 64) * head_dim * (dtype == SA_DTYPE_BF16 ? 2 : 4) < ((int64_t)1 << 31);
+// through buffer resources with 32-bit byte offsets: t rows `row` elements apart must stay below
+// 2 GiB.
+inline bool rows_fit(int64_t t, int64_t row, int dtype) {
+  return (t + 64) * row * (dtype == SA_DTYPE_BF16 ? 2 : 4) < ((int64_t)1 << 31);
 }
 
+
+// Element strides of a (sequence, head, row) view of a tensor whose head_dim elements per row are
+// contiguous: element (b, h, r, d) at p + b * seq + h * head + r * row + d.
+// (The row stride is 32-bit: one head's rows span less than 2 GiB, rows_fit.)
+struct Strides {
+  int64_t seq, head;
+  int row;
+  __host__ __device__ int64_t at(int64_t b, int64_t h) const { return b * seq + h * head; }
+};
 
 // One sa_forward call after its checks (pointers already typed by the storage dtype's entry).
 struct FwdCall {
   const void *q, *k, *v;
+  Strides qs, ks, vs;   // q, k, v views
+  void* y;              // optional storage-dtype copy of the output (NULL: none)
+  Strides ys;
   float *out, *rmax, *rden, *carry;
   const float* state_in;
   float* state_out;
   int64_t state_ld;
   void* ws;
   int nseq, H, Tq, Tk;
-  int64_t kvs;
   int q_off;
   float scale;
   int exempt, group, damp_mode;
@@ -157,10 +169,13 @@ struct FwdCall {
 // One sa_backward call after its checks.
 struct BwdCall {
   const void *q, *k, *v;
+  Strides qs, ks, vs;
   const float* out;
   const void* dout;
+  Strides dos;
   const float *rmax, *rden, *carry;
   void *dq, *dk, *dv, *ws;
+  Strides dqs, dks, dvs;
   int nseq, H, T;
   float scale;
   int exempt, group, grad_dtype, head_dim;

@@ -501,7 +501,8 @@ __device__ __forceinline__ float excl_scan32(float x) {
 template <class OP, int D>
 __global__ __launch_bounds__(NTHREADS) void sel_colsum_kernel(
     const typename OP::elem* __restrict__ q, const typename OP::elem* __restrict__ k,
-    float* __restrict__ colsum, int H, int Tq, int Tk, int64_t kvs, int q_off, int exempt, float scale, int RB) {
+    float* __restrict__ colsum, int H, int Tq, int Tk, Strides qs, Strides ks, int q_off, int exempt, float scale,
+    int RB) {
   using elem = typename OP::elem;
   using frag = typename OP::frag;
   constexpr int NS = D / OP::KS;
@@ -512,13 +513,13 @@ __global__ __launch_bounds__(NTHREADS) void sel_colsum_kernel(
   const int kb = blockIdx.x * NWAVES + wave;
   if (kb >= NKT) return;
   const int b = blockIdx.z;
-  const elem* q0 = q + (int64_t)b * H * Tq * D;
-  const elem* k0 = k + (int64_t)b * H * kvs;
+  const elem* q0 = q + qs.at(b, 0);
+  const elem* k0 = k + ks.at(b, 0);
   const int j = kb * TILE + n;
 
   frag kf[NS];
 #pragma unroll
-  for (int s = 0; s < NS; ++s) kf[s] = ld_std_bounded<OP>(k0, D, kb * TILE + n, Tk, h, s);
+  for (int s = 0; s < NS; ++s) kf[s] = ld_std_bounded<OP>(k0, ks.row, kb * TILE + n, Tk, h, s);
 
   const int rb_end = min(NBq, (int)(blockIdx.y + 1) * RB);
   for (int rb = blockIdx.y * RB; rb < rb_end; ++rb) {
@@ -528,7 +529,7 @@ __global__ __launch_bounds__(NTHREADS) void sel_colsum_kernel(
       f32x16 acc = zero16();
 #pragma unroll
       for (int s = 0; s < NS; ++s)
-        acc = OP::mma(ld_std_bounded<OP>(q0, D, rb * TILE + n, Tq, h, s), kf[s], acc);
+        acc = OP::mma(ld_std_bounded<OP>(q0, qs.row, rb * TILE + n, Tq, h, s), kf[s], acc);
 #pragma unroll
       for (int i = 0; i < 16; ++i) {
         const int r = rb * TILE + crow(i, h);
@@ -590,13 +591,16 @@ __global__ __launch_bounds__(NTHREADS) void sel_scan_kernel(
 template <class OP, int D, int G>
 constexpr int fwd_min_blocks() { return (sizeof(typename OP::elem) == 2 && D <= 64 && G == 1) ? SA_FWD_MIN_BLOCKS : 1; }
 
-template <class OP, int D, int G>
+// CV ("contiguous views"): q rows are D apart and its heads Tq * D apart, k rows D apart and its
+// heads ks.head apart -- the layout of sa_forward; the view strides are then compile-time facts
+// (fewer scalar registers live in the tile loop). Other views take the general instance.
+template <class OP, int D, int G, bool CV>
 __global__ __launch_bounds__(NTHREADS, (fwd_min_blocks<OP, D, G>())) void fwd_kernel(
     const typename OP::elem* __restrict__ q, const typename OP::elem* __restrict__ k,
     const typename OP::elem* __restrict__ vt, const float* __restrict__ carry,
     float* __restrict__ out, float* __restrict__ rmax, float* __restrict__ rden,
-    int H, int Tq, int Tk, int64_t kvs, int q_off, int64_t ldv, int exempt, float scale,
-    int damp_mode, float train_len) {
+    typename OP::elem* __restrict__ y, Strides ys, int H, int Tq, int Tk, Strides qs, Strides ks, int q_off,
+    int64_t ldv, int exempt, float scale, int damp_mode, float train_len) {
   using elem = typename OP::elem;
   using frag = typename OP::frag;
   constexpr int NS = D / OP::KS;          // MFMA steps over D
@@ -628,6 +632,16 @@ __global__ __launch_bounds__(NTHREADS, (fwd_min_blocks<OP, D, G>())) void fwd_ke
   const int q_rel = rb * TILE + n;
   const int q_abs = q_off + q_rel;
   const int64_t seq_row = (int64_t)b * H;   // row of head 0 of this sequence
+  auto q_head = [&](int hh) -> const elem* {
+    if constexpr (CV) return q + (seq_row + hh) * Tq * D;
+    else return q + qs.at(b, hh);
+  };
+  auto k_head = [&](int hh) -> const elem* {
+    if constexpr (CV) return k + (seq_row + hh) * ks.head;
+    else return k + ks.at(b, hh);
+  };
+  const int64_t q_ld = CV ? (int64_t)D : (int64_t)qs.row;
+  const int64_t k_ld = CV ? (int64_t)D : (int64_t)ks.row;
 
   auto kt_end_of = [&](int rbw) {
     const int last = q_off + rbw * TILE + TILE - 1;
@@ -641,14 +655,14 @@ __global__ __launch_bounds__(NTHREADS, (fwd_min_blocks<OP, D, G>())) void fwd_ke
   frag q0f[NS];
 #pragma unroll
   for (int g = 0; g < G; ++g) {
-    const elem* qh = q + (seq_row + hd0 + g) * Tq * D;
+    const elem* qh = q_head(hd0 + g);
 #pragma unroll
-    for (int s = 0; s < NS; ++s) qf[g][s] = ld_std_bounded<OP>(qh, D, q_rel, Tq, h, s);
+    for (int s = 0; s < NS; ++s) qf[g][s] = ld_std_bounded<OP>(qh, q_ld, q_rel, Tq, h, s);
   }
   if (!has_h0) {
-    const elem* qh = q + seq_row * Tq * D;
+    const elem* qh = q_head(0);
 #pragma unroll
-    for (int s = 0; s < NS; ++s) q0f[s] = ld_std_bounded<OP>(qh, D, q_rel, Tq, h, s);
+    for (int s = 0; s < NS; ++s) q0f[s] = ld_std_bounded<OP>(qh, q_ld, q_rel, Tq, h, s);
   }
 
   float m[G], l[G];
@@ -676,15 +690,20 @@ __global__ __launch_bounds__(NTHREADS, (fwd_min_blocks<OP, D, G>())) void fwd_ke
   // the workgroup's four query blocks (threads 0..127: wavefront w's row, key tid % 32).
   RowTile<elem, D> nK[NH];
   ColTile<elem, D> nVt[G];
+  const elem* k_rows[NH];   // the key rows of this workgroup's heads (outside the tile loop)
+#pragma unroll
+  for (int g = 0; g < G; ++g) k_rows[g] = k_head(hd0 + g);
+  k_rows[G] = k_head(0);
+  const int k_ldi = (int)k_ld;
   float nC = 0.f;
   auto load_tile = [&](int kt) {
     const int kbase = kt * TILE;
 #pragma unroll
     for (int g = 0; g < G; ++g) {
-      nK[g].load(k + (seq_row + hd0 + g) * kvs, D, kbase, Tk, tid);
+      nK[g].load(k_rows[g], k_ldi, kbase, Tk, tid);
       nVt[g].load(vt + (seq_row + hd0 + g) * D * ldv, ldv, kbase, tid);
     }
-    if (!has_h0) nK[G].load(k + seq_row * kvs, D, kbase, Tk, tid);
+    if (!has_h0) nK[G].load(k_rows[G], k_ldi, kbase, Tk, tid);
     const int w = (tid >> 5) & (NWAVES - 1);
     const int rbw = min(qsb * NWAVES + w, NBq - 1);
     const int jj = kbase + (tid & (TILE - 1));
@@ -829,13 +848,24 @@ __global__ __launch_bounds__(NTHREADS, (fwd_min_blocks<OP, D, G>())) void fwd_ke
     const float inv = 1.f / ltot;
     const int64_t row = (seq_row + hd0 + g) * Tq + q_rel;
     float* orow = out + row * D;
+    elem* yrow = y ? y + ys.at(b, hd0 + g) + (int64_t)q_rel * ys.row : nullptr;
 #pragma unroll
     for (int db = 0; db < DB; ++db) {
 #pragma unroll
       for (int a = 0; a < 4; ++a) {
         float4 v4 = make_float4(o[g][db][4 * a] * inv, o[g][db][4 * a + 1] * inv,
                                 o[g][db][4 * a + 2] * inv, o[g][db][4 * a + 3] * inv);
-        *reinterpret_cast<float4*>(orow + db * 32 + 8 * a + 4 * h) = v4;
+        const int d = db * 32 + 8 * a + 4 * h;
+        *reinterpret_cast<float4*>(orow + d) = v4;
+        if (yrow) {
+          if constexpr (sizeof(elem) == 2) {
+            *reinterpret_cast<uint2*>(yrow + d) = make_uint2(
+                (uint32_t)OP::to_elem(v4.x) | ((uint32_t)OP::to_elem(v4.y) << 16),
+                (uint32_t)OP::to_elem(v4.z) | ((uint32_t)OP::to_elem(v4.w) << 16));
+          } else {
+            *reinterpret_cast<float4*>(yrow + d) = v4;
+          }
+        }
       }
     }
     if (h == 0) {
@@ -852,7 +882,7 @@ __global__ __launch_bounds__(NTHREADS, (fwd_min_blocks<OP, D, G>())) void fwd_ke
 
 template <class OP, int D>
 __global__ __launch_bounds__(NTHREADS) void bwd_rowstats_kernel(
-    const typename OP::elem* __restrict__ dout, const float* __restrict__ out,
+    const typename OP::elem* __restrict__ dout, Strides dos, int H, int T, const float* __restrict__ out,
     const float* __restrict__ rmax, const float* __restrict__ rden,
     float* __restrict__ lse, float* __restrict__ dbar, int64_t rows) {
   using elem = typename OP::elem;
@@ -862,7 +892,8 @@ __global__ __launch_bounds__(NTHREADS) void bwd_rowstats_kernel(
   const int part = (int)(g % LPR);
   float acc = 0.f;
   if (r < rows) {
-    const elem* dr = dout + r * D + part * 8;
+    const int64_t hr = r / T;   // b * H + head
+    const elem* dr = dout + dos.at(hr / H, hr % H) + (r - hr * T) * dos.row + part * 8;
     const float* orow = out + r * D + part * 8;
     const float4 o0 = *reinterpret_cast<const float4*>(orow);
     const float4 o1 = *reinterpret_cast<const float4*>(orow + 4);
@@ -885,21 +916,22 @@ __global__ __launch_bounds__(NTHREADS) void bwd_rowstats_kernel(
   }
 }
 
-// in (R, T, D) -> outT (R, D, ldt), zero past T; a workgroup moves a [64 t][D] slab through LDS in
-// 16-byte chunks: row chunks in, then 8 (bf16) or 4 (fp32) consecutive t of one d out.
+// in (R = nseq * H views of T rows, Strides is) -> outT (R, D, ldt), zero past T; a workgroup moves
+// a [64 t][D] slab through LDS in 16-byte chunks: row chunks in, then 8 (bf16) or 4 (fp32)
+// consecutive t of one d out.
 template <typename E, int D>
 __global__ __launch_bounds__(NTHREADS) void transpose_kernel(const E* __restrict__ in, E* __restrict__ outT,
-                                                             int T, int64_t ldt, int64_t in_stride) {
+                                                             int T, int64_t ldt, Strides is, int H) {
   constexpr int EPC = 16 / (int)sizeof(E);
   constexpr int LDS_LD = D + EPC;   // padded row: 16-byte aligned, rows on shifted banks
   __shared__ __attribute__((aligned(16))) E tile[64 * LDS_LD];
   const int64_t r = blockIdx.y;
   const int t0 = blockIdx.x * 64;
-  const E* src = in + r * in_stride;
+  const E* src = in + is.at(r / H, r % H);
   for (int c = threadIdx.x; c < 64 * D / EPC; c += NTHREADS) {
     const int tt = c / (D / EPC), d0 = (c % (D / EPC)) * EPC;
     uint4 v = make_uint4(0u, 0u, 0u, 0u);
-    if (t0 + tt < T) v = *reinterpret_cast<const uint4*>(src + (int64_t)(t0 + tt) * D + d0);
+    if (t0 + tt < T) v = *reinterpret_cast<const uint4*>(src + (int64_t)(t0 + tt) * is.row + d0);
     *reinterpret_cast<uint4*>(&tile[tt * LDS_LD + d0]) = v;
   }
   __syncthreads();
@@ -1078,14 +1110,15 @@ __device__ __forceinline__ bool big_tile(const f32x16& x) {
 // query tile into ucheck[gi][b][qb][j] for the dQ kernel. Head 0's dK gets g = -gate*U from every
 // group: the group holding head 0 folds it into head 0's dz; the others add their share to dk0x.
 
-template <class OP, int D, int G>
+// CV: every view is the contiguous (nseq, H, T, D) layout of sa_backward (see fwd_kernel).
+template <class OP, int D, int G, bool CV>
 __global__ __launch_bounds__(NTHREADS, (kv_min_blocks<OP, D, G>())) void bwd_kv_kernel(
     const typename OP::elem* __restrict__ q, const typename OP::elem* __restrict__ k,
     const typename OP::elem* __restrict__ v, const typename OP::elem* __restrict__ qt,
-    const typename OP::elem* __restrict__ dout, const typename OP::elem* __restrict__ dot,
-    const float* __restrict__ lse, const float* __restrict__ dbar, const float* __restrict__ carry,
-    float* __restrict__ ucheck, float* __restrict__ dk, float* __restrict__ dv, float* __restrict__ dk0x,
-    int nseq, int H, int T, int64_t ldt, int exempt, float scale) {
+    const typename OP::elem* __restrict__ dout, const typename OP::elem* __restrict__ dot, Strides qs,
+    Strides ks, Strides vs, Strides dos, const float* __restrict__ lse, const float* __restrict__ dbar,
+    const float* __restrict__ carry, float* __restrict__ ucheck, float* __restrict__ dk, float* __restrict__ dv,
+    float* __restrict__ dk0x, int nseq, int H, int T, int64_t ldt, int exempt, float scale) {
   using elem = typename OP::elem;
   using frag = typename OP::frag;
   constexpr int NS = D / OP::KS;
@@ -1124,6 +1157,15 @@ __global__ __launch_bounds__(NTHREADS, (kv_min_blocks<OP, D, G>())) void bwd_kv_
   const int key0 = bxy.x * (NWAVES * TILE) + wave * TILE;
   const int j = key0 + n;
   const int64_t seq_row = (int64_t)b * H;
+  // view accessors (CV: the contiguous layout, strides as compile-time facts)
+  auto view_head = [&](const elem* base, const Strides& vs_, int hh) -> const elem* {
+    if constexpr (CV) return base + (seq_row + hh) * T * D;
+    else return base + vs_.at(b, hh);
+  };
+  auto view_ld = [&](const Strides& vs_) -> int64_t {
+    if constexpr (CV) return D;
+    else return vs_.row;
+  };
   float* uplane = ucheck + ((int64_t)gi * nseq + b) * NB * (int64_t)T;
   const float* carry_col = carry + (int64_t)b * NB * T + (j < T ? j : 0);
 
@@ -1136,33 +1178,33 @@ __global__ __launch_bounds__(NTHREADS, (kv_min_blocks<OP, D, G>())) void bwd_kv_
       const int r = c / CPR, cc = c % CPR;
       const int64_t jr = min(key0 + r, T - 1);
       const bool ok = key0 + r < T;
-      auto put = [&](int x, const elem* src) {
-        const uint4 v4 = *reinterpret_cast<const uint4*>(src + jr * D + cc * 8);
+      auto put = [&](int x, const elem* src, int64_t ld) {
+        const uint4 v4 = *reinterpret_cast<const uint4*>(src + jr * ld + cc * 8);
         *reinterpret_cast<uint4*>(&sKV[wave][x][swz64(r, cc)]) =
             make_uint4(ok ? v4.x : 0u, ok ? v4.y : 0u, ok ? v4.z : 0u, ok ? v4.w : 0u);
       };
 #pragma unroll
       for (int g = 0; g < G; ++g) {
-        put(2 * g, k + (seq_row + hd0 + g) * T * D);
-        put(2 * g + 1, v + (seq_row + hd0 + g) * T * D);
+        put(2 * g, view_head(k, ks, hd0 + g), view_ld(ks));
+        put(2 * g + 1, view_head(v, vs, hd0 + g), view_ld(vs));
       }
-      if (!has_h0) put(2 * G, k + seq_row * T * D);
+      if (!has_h0) put(2 * G, view_head(k, ks, 0), view_ld(ks));
     }
   } else {
 #pragma unroll
     for (int g = 0; g < G; ++g) {
-      const elem* kh = k + (seq_row + hd0 + g) * T * D;
-      const elem* vh = v + (seq_row + hd0 + g) * T * D;
+      const elem* kh = view_head(k, ks, hd0 + g);
+      const elem* vh = view_head(v, vs, hd0 + g);
 #pragma unroll
       for (int s = 0; s < NS; ++s) {
-        kf[g][s] = ld_std_bounded<OP>(kh, D, j, T, h, s);
-        vf[g][s] = ld_std_bounded<OP>(vh, D, j, T, h, s);
+        kf[g][s] = ld_std_bounded<OP>(kh, view_ld(ks), j, T, h, s);
+        vf[g][s] = ld_std_bounded<OP>(vh, view_ld(vs), j, T, h, s);
       }
     }
     if (!has_h0) {
-      const elem* kh = k + seq_row * T * D;
+      const elem* kh = view_head(k, ks, 0);
 #pragma unroll
-      for (int s = 0; s < NS; ++s) k0f[s] = ld_std_bounded<OP>(kh, D, j, T, h, s);
+      for (int s = 0; s < NS; ++s) k0f[s] = ld_std_bounded<OP>(kh, view_ld(ks), j, T, h, s);
     }
   }
   // fragment s of row n (this lane's key) of LDS row block x
@@ -1206,14 +1248,24 @@ __global__ __launch_bounds__(NTHREADS, (kv_min_blocks<OP, D, G>())) void bwd_kv_
   RowTile<elem, D> nQ[NH], ndO[G];
   ColTile<elem, D> nQt[NH], ndOt[G];
   float nLse[G], nDb[G];
+  // the query-side rows of this workgroup's heads (computed once, outside the tile loop)
+  const elem* q_rows[NH];
+  const elem* do_rows[G];
+#pragma unroll
+  for (int g = 0; g < G; ++g) {
+    q_rows[g] = view_head(q, qs, hd0 + g);
+    do_rows[g] = view_head(dout, dos, hd0 + g);
+  }
+  q_rows[G] = view_head(q, qs, 0);
+  const int q_ld = (int)view_ld(qs), do_ld = (int)view_ld(dos);
   auto load_tile = [&](int qb) {
     const int qbase = qb * TILE;
 #pragma unroll
     for (int g = 0; g < G; ++g) {
       const int64_t row = seq_row + hd0 + g;
-      nQ[g].load(q + row * T * D, D, qbase, T, tid);
+      nQ[g].load(q_rows[g], q_ld, qbase, T, tid);
       nQt[g].load(qt + row * D * ldt, ldt, qbase, tid);
-      ndO[g].load(dout + row * T * D, D, qbase, T, tid);
+      ndO[g].load(do_rows[g], do_ld, qbase, T, tid);
       ndOt[g].load(dot + row * D * ldt, ldt, qbase, tid);
       const int r = qbase + (tid & (TILE - 1));
       const int rr = min(r, T - 1);
@@ -1222,7 +1274,7 @@ __global__ __launch_bounds__(NTHREADS, (kv_min_blocks<OP, D, G>())) void bwd_kv_
       nDb[g] = r < T ? -dv_ : 0.f;   // negated: the dO.v product accumulates onto it
     }
     if (!has_h0) {
-      nQ[G].load(q + seq_row * T * D, D, qbase, T, tid);
+      nQ[G].load(q_rows[G], q_ld, qbase, T, tid);
       nQt[G].load(qt + seq_row * D * ldt, ldt, qbase, tid);
     }
   };
@@ -1405,13 +1457,14 @@ __global__ __launch_bounds__(NTHREADS, (kv_min_blocks<OP, D, G>())) void bwd_kv_
 // the suffix inside the tile. dQ = dz K takes dz through a per-wavefront LDS tile (as the A operand)
 // and K^T from LDS (as the B operand).
 
-template <class OP, int D, int G>
+template <class OP, int D, int G, bool CV>   // CV: see bwd_kv_kernel
 __global__ __launch_bounds__(NTHREADS, (dq_min_blocks<OP, D>())) void bwd_dq_kernel(
     const typename OP::elem* __restrict__ q, const typename OP::elem* __restrict__ k,
     const typename OP::elem* __restrict__ v, const typename OP::elem* __restrict__ kt,
-    const typename OP::elem* __restrict__ dout, const float* __restrict__ lse, const float* __restrict__ dbar,
-    const float* __restrict__ carry, const float* __restrict__ ucheck, float* __restrict__ dq,
-    float* __restrict__ dq0x, int nseq, int H, int T, int64_t ldt, int exempt, float scale) {
+    const typename OP::elem* __restrict__ dout, Strides qs, Strides ks, Strides vs, Strides dos,
+    const float* __restrict__ lse, const float* __restrict__ dbar, const float* __restrict__ carry,
+    const float* __restrict__ ucheck, float* __restrict__ dq, float* __restrict__ dq0x, int nseq, int H, int T,
+    int64_t ldt, int exempt, float scale) {
   using elem = typename OP::elem;
   using frag = typename OP::frag;
   constexpr int NS = D / OP::KS;
@@ -1451,6 +1504,15 @@ __global__ __launch_bounds__(NTHREADS, (dq_min_blocks<OP, D>())) void bwd_dq_ker
   const int qb = qsb * NWAVES + wave;
   const int qbase = qb * TILE;
   const int64_t seq_row = (int64_t)b * H;
+  // view accessors (CV: the contiguous layout, strides as compile-time facts)
+  auto view_head = [&](const elem* base, const Strides& vs_, int hh) -> const elem* {
+    if constexpr (CV) return base + (seq_row + hh) * T * D;
+    else return base + vs_.at(b, hh);
+  };
+  auto view_ld = [&](const Strides& vs_) -> int64_t {
+    if constexpr (CV) return D;
+    else return vs_.row;
+  };
   const int my_end = (qb < NB) ? qb + 1 : 0;
   const int wg_end = min(qsb * NWAVES + NWAVES - 1, NB - 1) + 1;
   elem* zs = sZ[wave];
@@ -1466,24 +1528,24 @@ __global__ __launch_bounds__(NTHREADS, (dq_min_blocks<OP, D>())) void bwd_dq_ker
   if constexpr (!QLDS) {
 #pragma unroll
     for (int g = 0; g < G; ++g) {
-      const int64_t row = seq_row + hd0 + g;
 #pragma unroll
       for (int s = 0; s < NS; ++s) {
-        qa[g][s] = ld_std_bounded<OP>(q + row * T * D, D, qbase + n, T, h, s);
-        doa[g][s] = ld_std_bounded<OP>(dout + row * T * D, D, qbase + n, T, h, s);
+        qa[g][s] = ld_std_bounded<OP>(view_head(q, qs, hd0 + g), view_ld(qs), qbase + n, T, h, s);
+        doa[g][s] = ld_std_bounded<OP>(view_head(dout, dos, hd0 + g), view_ld(dos), qbase + n, T, h, s);
       }
     }
   } else {
     constexpr int EPC = 16 / (int)sizeof(elem), CPR = D / EPC;
 #pragma unroll
     for (int g = 0; g < G; ++g) {
-      const int64_t row = seq_row + hd0 + g;
+      const elem* qh = view_head(q, qs, hd0 + g);
+      const elem* doh = view_head(dout, dos, hd0 + g);
       for (int c = lane; c < TILE * CPR; c += 64) {
         const int r = c / CPR, cc = (c % CPR) * EPC;
         const int rr = min(qbase + r, T - 1);
         const bool ok = qbase + r < T;
-        const uint4 xq = *reinterpret_cast<const uint4*>(q + (row * T + rr) * D + cc);
-        const uint4 xo = *reinterpret_cast<const uint4*>(dout + (row * T + rr) * D + cc);
+        const uint4 xq = *reinterpret_cast<const uint4*>(qh + rr * view_ld(qs) + cc);
+        const uint4 xo = *reinterpret_cast<const uint4*>(doh + rr * view_ld(dos) + cc);
         *reinterpret_cast<uint4*>(&sQw[wave][g][r * LDK + cc]) =
             ok ? xq : make_uint4(0u, 0u, 0u, 0u);
         *reinterpret_cast<uint4*>(&sdOw[wave][g][r * LDK + cc]) =
@@ -1510,7 +1572,7 @@ __global__ __launch_bounds__(NTHREADS, (dq_min_blocks<OP, D>())) void bwd_dq_ker
   }
   if (!has_h0) {
 #pragma unroll
-    for (int s = 0; s < NS; ++s) q0a[s] = ld_std_bounded<OP>(q + seq_row * T * D, D, qbase + n, T, h, s);
+    for (int s = 0; s < NS; ++s) q0a[s] = ld_std_bounded<OP>(view_head(q, qs, 0), view_ld(qs), qbase + n, T, h, s);
   }
 
   f32x16 dqacc[G][DB], dq0acc[DB];
@@ -1527,17 +1589,27 @@ __global__ __launch_bounds__(NTHREADS, (dq_min_blocks<OP, D>())) void bwd_dq_ker
   // Staging of one key tile: K, V, K^T of the group (+ head 0's K, K^T).
   RowTile<elem, D> nK[NH], nV[G];
   ColTile<elem, D> nKt[NH];
+  // the key-side rows of this workgroup's heads (computed once, outside the tile loop)
+  const elem* k_rows[NH];
+  const elem* v_rows[G];
+#pragma unroll
+  for (int g = 0; g < G; ++g) {
+    k_rows[g] = view_head(k, ks, hd0 + g);
+    v_rows[g] = view_head(v, vs, hd0 + g);
+  }
+  k_rows[G] = view_head(k, ks, 0);
+  const int k_ld = (int)view_ld(ks), v_ld = (int)view_ld(vs);
   auto load_tile = [&](int ktile) {
     const int kbase = ktile * TILE;
 #pragma unroll
     for (int g = 0; g < G; ++g) {
       const int64_t row = seq_row + hd0 + g;
-      nK[g].load(k + row * T * D, D, kbase, T, tid);
-      nV[g].load(v + row * T * D, D, kbase, T, tid);
+      nK[g].load(k_rows[g], k_ld, kbase, T, tid);
+      nV[g].load(v_rows[g], v_ld, kbase, T, tid);
       nKt[g].load(kt + row * D * ldt, ldt, kbase, tid);
     }
     if (!has_h0) {
-      nK[G].load(k + seq_row * T * D, D, kbase, T, tid);
+      nK[G].load(k_rows[G], k_ld, kbase, T, tid);
       nKt[G].load(kt + seq_row * D * ldt, ldt, kbase, tid);
     }
   };
@@ -1745,22 +1817,26 @@ __global__ __launch_bounds__(NTHREADS, (dq_min_blocks<OP, D>())) void bwd_dq_ker
 __device__ __forceinline__ void store_grad(uint16_t* p, float x) { *p = OpBF16::to_elem(x); }
 __device__ __forceinline__ void store_grad(float* p, float x) { *p = x; }
 
+// The fp32 sums are (b * H + head, t, D) contiguous; the outputs are views (Strides).
 template <typename OUT>
 __global__ __launch_bounds__(NTHREADS) void bwd_finish_kernel(
     const float* __restrict__ dq32, const float* __restrict__ dk32, const float* __restrict__ dv32,
     const float* __restrict__ dq0x, const float* __restrict__ dk0x, OUT* __restrict__ dq, OUT* __restrict__ dk,
-    OUT* __restrict__ dv, int H, int64_t TD, int64_t total, float scale) {
+    OUT* __restrict__ dv, Strides dqs, Strides dks, Strides dvs, int H, int D, int64_t TD, int64_t total,
+    float scale) {
   for (int64_t e = (int64_t)blockIdx.x * NTHREADS + threadIdx.x; e < total; e += (int64_t)gridDim.x * NTHREADS) {
     const int64_t row = e / TD;          // b*H + head
     const int64_t off = e - row * TD;
+    const int64_t b = row / H, hd = row - b * H;
+    const int64_t t = off / D, d = off - t * D;
     float qv = dq32[e], kv = dk32[e];
-    if (row % H == 0) {
-      qv += dq0x[(row / H) * TD + off];
-      kv += dk0x[(row / H) * TD + off];
+    if (hd == 0) {
+      qv += dq0x[b * TD + off];
+      kv += dk0x[b * TD + off];
     }
-    store_grad(dq + e, qv * scale);
-    store_grad(dk + e, kv);
-    store_grad(dv + e, dv32[e]);
+    store_grad(dq + dqs.at(b, hd) + t * dqs.row + d, qv * scale);
+    store_grad(dk + dks.at(b, hd) + t * dks.row + d, kv);
+    store_grad(dv + dvs.at(b, hd) + t * dvs.row + d, dv32[e]);
   }
 }
 
@@ -2072,100 +2148,107 @@ __global__ __launch_bounds__(NTHREADS) void decode_finish_kernel(
 // Host side: launch sequences of one storage dtype and head dim.
 
 template <class OP, int D>
-int run_selection(const typename OP::elem* q, const typename OP::elem* k, float* carry, const float* state_in,
-                  float* state_out, int64_t state_ld, int nseq, int H, int Tq, int Tk, int64_t kvs, int q_off,
-                  int exempt, float scale, hipStream_t st) {
-  const int NBq = (int)cdiv(Tq, TILE), NKT = (int)cdiv(Tk, TILE);
+int run_selection(const FwdCall& c, hipStream_t st) {
+  using elem = typename OP::elem;
+  const int NBq = (int)cdiv(c.Tq, TILE), NKT = (int)cdiv(c.Tk, TILE);
   const int RB = 8;
-  dim3 g1((unsigned)cdiv(NKT, NWAVES), (unsigned)cdiv(NBq, RB), (unsigned)nseq);
+  dim3 g1((unsigned)cdiv(NKT, NWAVES), (unsigned)cdiv(NBq, RB), (unsigned)c.nseq);
   TimedLaunch timed(SA_KERNEL_SELECTION, st);
-  hipLaunchKernelGGL((sel_colsum_kernel<OP, D>), g1, dim3(NTHREADS), 0, st, q, k, carry, H, Tq, Tk, kvs, q_off,
-                     exempt, scale, RB);
-  dim3 g2((unsigned)cdiv(Tk, NTHREADS), (unsigned)nseq);
-  hipLaunchKernelGGL(sel_scan_kernel, g2, dim3(NTHREADS), 0, st, carry, state_in, state_out, state_ld, NBq, Tk,
-                     q_off);
+  hipLaunchKernelGGL((sel_colsum_kernel<OP, D>), g1, dim3(NTHREADS), 0, st, static_cast<const elem*>(c.q),
+                     static_cast<const elem*>(c.k), c.carry, c.H, c.Tq, c.Tk, c.qs, c.ks, c.q_off, c.exempt, c.scale,
+                     RB);
+  dim3 g2((unsigned)cdiv(c.Tk, NTHREADS), (unsigned)c.nseq);
+  hipLaunchKernelGGL(sel_scan_kernel, g2, dim3(NTHREADS), 0, st, c.carry, c.state_in, c.state_out, c.state_ld, NBq,
+                     c.Tk, c.q_off);
   return launch_status();
 }
 
 template <class OP, int D, int G>
-void launch_fwd(const typename OP::elem* q, const typename OP::elem* k, const typename OP::elem* vt,
-                const float* carry, float* out, float* rmax, float* rden, int nseq, int H, int Tq, int Tk,
-                int64_t kvs, int q_off, int64_t ldv, int exempt, float scale, int damp_mode, float train_len,
-                hipStream_t st) {
-  const int NBq = (int)cdiv(Tq, TILE);
-  dim3 grid((unsigned)cdiv(NBq, NWAVES), (unsigned)(nseq * (H / G)));
-  TimedLaunch timed(SA_KERNEL_FORWARD, st);
-  hipLaunchKernelGGL((fwd_kernel<OP, D, G>), grid, dim3(NTHREADS), 0, st, q, k, vt, carry, out, rmax, rden, H, Tq,
-                     Tk, kvs, q_off, ldv, exempt, scale, damp_mode, train_len);
+void launch_fwd(const FwdCall& c, const typename OP::elem* vt, int64_t ldv) {
+  using elem = typename OP::elem;
+  const int NBq = (int)cdiv(c.Tq, TILE);
+  dim3 grid((unsigned)cdiv(NBq, NWAVES), (unsigned)(c.nseq * (c.H / G)));
+  // the layout of sa_forward: q contiguous, k rows D apart, k's sequences H heads apart
+  const bool cv = c.qs.row == D && c.qs.head == (int64_t)c.Tq * D && c.qs.seq == (int64_t)c.H * c.qs.head &&
+                  c.ks.row == D && c.ks.seq == (int64_t)c.H * c.ks.head;
+  TimedLaunch timed(SA_KERNEL_FORWARD, c.st);
+#define SA_LAUNCH_FWD(CVV)                                                                                        \
+  hipLaunchKernelGGL((fwd_kernel<OP, D, G, CVV>), grid, dim3(NTHREADS), 0, c.st, static_cast<const elem*>(c.q),  \
+                     static_cast<const elem*>(c.k), vt, c.carry, c.out, c.rmax, c.rden, static_cast<elem*>(c.y),  \
+                     c.ys, c.H, c.Tq, c.Tk, c.qs, c.ks, c.q_off, ldv, c.exempt, c.scale, c.damp_mode, c.train_len)
+  if (cv) SA_LAUNCH_FWD(true);
+  else SA_LAUNCH_FWD(false);
+#undef SA_LAUNCH_FWD
 }
 
 template <class OP, int D>
-int forward_impl(const void* q_, const void* k_, const void* v_, float* out, float* rmax, float* rden,
-                 float* carry, const float* state_in, float* state_out, int64_t state_ld, void* ws, int nseq,
-                 int H, int Tq, int Tk, int64_t kvs, int q_off, float scale, int exempt, int group, int damp_mode,
-                 float train_len, hipStream_t st) {
+int forward_impl(const FwdCall& c) {
   using elem = typename OP::elem;
-  const elem* q = static_cast<const elem*>(q_);
-  const elem* k = static_cast<const elem*>(k_);
-  const elem* v = static_cast<const elem*>(v_);
-  const int64_t ldv = sa_transposed_ld(Tk);
-  elem* vt = static_cast<elem*>(ws);
-  dim3 gt((unsigned)cdiv(ldv, 64), (unsigned)(nseq * H));
-  hipLaunchKernelGGL((transpose_kernel<elem, D>), gt, dim3(NTHREADS), 0, st, v, vt, Tk, ldv, kvs);
-  int rc = run_selection<OP, D>(q, k, carry, state_in, state_out, state_ld, nseq, H, Tq, Tk, kvs, q_off, exempt,
-                                scale, st);
+  const int64_t ldv = sa_transposed_ld(c.Tk);
+  elem* vt = static_cast<elem*>(c.ws);
+  dim3 gt((unsigned)cdiv(ldv, 64), (unsigned)(c.nseq * c.H));
+  hipLaunchKernelGGL((transpose_kernel<elem, D>), gt, dim3(NTHREADS), 0, c.st, static_cast<const elem*>(c.v), vt,
+                     c.Tk, ldv, c.vs, c.H);
+  int rc = run_selection<OP, D>(c, c.st);
   if (rc) return rc;
   const int dtype = sizeof(elem) == 2 ? SA_DTYPE_BF16 : SA_DTYPE_F32;
-  const int G = auto_group(dtype, D, H, group, false);
+  const int G = auto_group(dtype, D, c.H, c.group, false);
   if (G == 4) {
-    if constexpr (sizeof(elem) == 2 && D <= 64)
-      launch_fwd<OP, D, 4>(q, k, vt, carry, out, rmax, rden, nseq, H, Tq, Tk, kvs, q_off, ldv, exempt, scale, damp_mode,
-                           train_len, st);
+    if constexpr (sizeof(elem) == 2 && D <= 64) launch_fwd<OP, D, 4>(c, vt, ldv);
   } else if (G == 2) {
-    if constexpr (sizeof(elem) == 2 && D <= 64)
-      launch_fwd<OP, D, 2>(q, k, vt, carry, out, rmax, rden, nseq, H, Tq, Tk, kvs, q_off, ldv, exempt, scale, damp_mode,
-                           train_len, st);
+    if constexpr (sizeof(elem) == 2 && D <= 64) launch_fwd<OP, D, 2>(c, vt, ldv);
   } else {
-    launch_fwd<OP, D, 1>(q, k, vt, carry, out, rmax, rden, nseq, H, Tq, Tk, kvs, q_off, ldv, exempt, scale, damp_mode,
-                         train_len, st);
+    launch_fwd<OP, D, 1>(c, vt, ldv);
   }
   return launch_status();
 }
 
 template <class OP, int D, int G>
-void launch_bwd(const typename OP::elem* q, const typename OP::elem* k, const typename OP::elem* v,
-                const typename OP::elem* qt, const typename OP::elem* kt, const typename OP::elem* dout,
-                const typename OP::elem* dot, const float* lse, const float* dbar, const float* carry, float* ucheck,
-                float* dq, float* dk, float* dv, float* dq0x, float* dk0x, int nseq, int H, int T, int64_t ldt,
-                int exempt, float scale, hipStream_t st) {
-  dim3 grid((unsigned)cdiv(T, NWAVES * TILE), (unsigned)(nseq * (H / G)));
+void launch_bwd(const BwdCall& c, const typename OP::elem* qt, const typename OP::elem* kt,
+                const typename OP::elem* dot, const float* lse, const float* dbar, float* ucheck, float* dq,
+                float* dk, float* dv, float* dq0x, float* dk0x, int64_t ldt) {
+  using elem = typename OP::elem;
+  const elem* q = static_cast<const elem*>(c.q);
+  const elem* k = static_cast<const elem*>(c.k);
+  const elem* v = static_cast<const elem*>(c.v);
+  const elem* dout = static_cast<const elem*>(c.dout);
+  dim3 grid((unsigned)cdiv(c.T, NWAVES * TILE), (unsigned)(c.nseq * (c.H / G)));
+  // every view the contiguous (nseq, H, T, D) layout of sa_backward
+  auto contiguous = [&](const Strides& s) {
+    return s.row == D && s.head == (int64_t)c.T * D && s.seq == (int64_t)c.H * s.head;
+  };
+  const bool cv = contiguous(c.qs) && contiguous(c.ks) && contiguous(c.vs) && contiguous(c.dos);
+#define SA_LAUNCH_KV(CVV)                                                                                         \
+  hipLaunchKernelGGL((bwd_kv_kernel<OP, D, G, CVV>), grid, dim3(NTHREADS), 0, c.st, q, k, v, qt, dout, dot, c.qs, \
+                     c.ks, c.vs, c.dos, lse, dbar, c.carry, ucheck, dk, dv, dk0x, c.nseq, c.H, c.T, ldt, c.exempt,  \
+                     c.scale)
+#define SA_LAUNCH_DQ(CVV)                                                                                         \
+  hipLaunchKernelGGL((bwd_dq_kernel<OP, D, G, CVV>), grid, dim3(NTHREADS), 0, c.st, q, k, v, kt, dout, c.qs, c.ks, \
+                     c.vs, c.dos, lse, dbar, c.carry, ucheck, dq, dq0x, c.nseq, c.H, c.T, ldt, c.exempt, c.scale)
   {
-    TimedLaunch timed(SA_KERNEL_BACKWARD, st);
-    hipLaunchKernelGGL((bwd_kv_kernel<OP, D, G>), grid, dim3(NTHREADS), 0, st, q, k, v, qt, dout, dot, lse, dbar,
-                       carry, ucheck, dk, dv, dk0x, nseq, H, T, ldt, exempt, scale);
+    TimedLaunch timed(SA_KERNEL_BACKWARD, c.st);
+    if (cv) SA_LAUNCH_KV(true);
+    else SA_LAUNCH_KV(false);
   }
   {
-    TimedLaunch timed(SA_KERNEL_BACKWARD_DQ, st);
-    hipLaunchKernelGGL((bwd_dq_kernel<OP, D, G>), grid, dim3(NTHREADS), 0, st, q, k, v, kt, dout, lse, dbar, carry,
-                       ucheck, dq, dq0x, nseq, H, T, ldt, exempt, scale);
+    TimedLaunch timed(SA_KERNEL_BACKWARD_DQ, c.st);
+    if (cv) SA_LAUNCH_DQ(true);
+    else SA_LAUNCH_DQ(false);
   }
+#undef SA_LAUNCH_KV
+#undef SA_LAUNCH_DQ
 }
 
 template <class OP, int D>
-int backward_impl(const void* q_, const void* k_, const void* v_, const float* out, const void* dout_,
-                  const float* rmax, const float* rden, const float* carry, void* dq_, void* dk_, void* dv_,
-                  void* ws, int nseq, int H, int T, float scale, int exempt, int group, int grad_dtype,
-                  hipStream_t st) {
+int backward_impl(const BwdCall& c) {
   using elem = typename OP::elem;
-  const elem* q = static_cast<const elem*>(q_);
-  const elem* k = static_cast<const elem*>(k_);
-  const elem* v = static_cast<const elem*>(v_);
-  const elem* dout = static_cast<const elem*>(dout_);
+  const int nseq = c.nseq, H = c.H, T = c.T;
+  const hipStream_t st = c.st;
   const int dtype = sizeof(elem) == 2 ? SA_DTYPE_BF16 : SA_DTYPE_F32;
-  const int G = bwd_group(dtype, D, H, group);
+  const int G = bwd_group(dtype, D, H, c.group);
   const int64_t R = (int64_t)nseq * H, ldt = sa_transposed_ld(T);
   const BwdLayout L = bwd_layout(nseq, H, T, D, sizeof(elem), G);
-  char* base = static_cast<char*>(ws);
+  char* base = static_cast<char*>(c.ws);
   elem* qt = reinterpret_cast<elem*>(base + L.qt);
   elem* dot = reinterpret_cast<elem*>(base + L.dot);
   elem* kt = reinterpret_cast<elem*>(base + L.kt);
@@ -2177,21 +2260,22 @@ int backward_impl(const void* q_, const void* k_, const void* v_, const float* o
   float* dq0x = reinterpret_cast<float*>(base + L.dq0x);
   float* dk0x = reinterpret_cast<float*>(base + L.dk0x);
   float* ucheck = reinterpret_cast<float*>(base + L.ucheck);
+  const elem* q = static_cast<const elem*>(c.q);
+  const elem* k = static_cast<const elem*>(c.k);
+  const elem* dout = static_cast<const elem*>(c.dout);
 
   dim3 gt((unsigned)cdiv(ldt, 64), (unsigned)R);
-  hipLaunchKernelGGL((transpose_kernel<elem, D>), gt, dim3(NTHREADS), 0, st, q, qt, T, ldt, (int64_t)T * D);
-  hipLaunchKernelGGL((transpose_kernel<elem, D>), gt, dim3(NTHREADS), 0, st, dout, dot, T, ldt, (int64_t)T * D);
-  hipLaunchKernelGGL((transpose_kernel<elem, D>), gt, dim3(NTHREADS), 0, st, k, kt, T, ldt, (int64_t)T * D);
+  hipLaunchKernelGGL((transpose_kernel<elem, D>), gt, dim3(NTHREADS), 0, st, q, qt, T, ldt, c.qs, H);
+  hipLaunchKernelGGL((transpose_kernel<elem, D>), gt, dim3(NTHREADS), 0, st, dout, dot, T, ldt, c.dos, H);
+  hipLaunchKernelGGL((transpose_kernel<elem, D>), gt, dim3(NTHREADS), 0, st, k, kt, T, ldt, c.ks, H);
   hipLaunchKernelGGL((bwd_rowstats_kernel<OP, D>), dim3((unsigned)cdiv(R * T * (D / 8), NTHREADS)), dim3(NTHREADS),
-                     0, st, dout, out, rmax, rden, lse, dbar, R * T);
+                     0, st, dout, c.dos, H, T, c.out, c.rmax, c.rden, lse, dbar, R * T);
   // head 0's shares from the other groups are atomic targets (one add per element and group)
   hipLaunchKernelGGL(fill_zero_kernel, dim3(256), dim3(NTHREADS), 0, st, reinterpret_cast<float4*>(dq0x),
                      (int64_t)((int64_t)nseq * T * D / 4));
   hipLaunchKernelGGL(fill_zero_kernel, dim3(256), dim3(NTHREADS), 0, st, reinterpret_cast<float4*>(dk0x),
                      (int64_t)((int64_t)nseq * T * D / 4));
-#define SA_LAUNCH_BWD(GG)                                                                                          \
-  launch_bwd<OP, D, GG>(q, k, v, qt, kt, dout, dot, lse, dbar, carry, ucheck, dq32, dk32, dv32, dq0x, dk0x, nseq, H, \
-                        T, ldt, exempt, scale, st)
+#define SA_LAUNCH_BWD(GG) launch_bwd<OP, D, GG>(c, qt, kt, dot, lse, dbar, ucheck, dq32, dk32, dv32, dq0x, dk0x, ldt)
   if constexpr (sizeof(elem) == 2 && D <= 32) {
     if (G == 2) SA_LAUNCH_BWD(2);
     else SA_LAUNCH_BWD(1);
@@ -2201,14 +2285,14 @@ int backward_impl(const void* q_, const void* k_, const void* v_, const float* o
 #undef SA_LAUNCH_BWD
   const int64_t total = R * T * D;
   const dim3 fgrid((unsigned)std::min<int64_t>(cdiv(total, NTHREADS), 8192));
-  if (grad_dtype == SA_DTYPE_F32)
+  if (c.grad_dtype == SA_DTYPE_F32)
     hipLaunchKernelGGL((bwd_finish_kernel<float>), fgrid, dim3(NTHREADS), 0, st, dq32, dk32, dv32, dq0x, dk0x,
-                       static_cast<float*>(dq_), static_cast<float*>(dk_), static_cast<float*>(dv_), H,
-                       (int64_t)T * D, total, scale);
+                       static_cast<float*>(c.dq), static_cast<float*>(c.dk), static_cast<float*>(c.dv), c.dqs, c.dks,
+                       c.dvs, H, D, (int64_t)T * D, total, c.scale);
   else
     hipLaunchKernelGGL((bwd_finish_kernel<uint16_t>), fgrid, dim3(NTHREADS), 0, st, dq32, dk32, dv32, dq0x, dk0x,
-                       static_cast<uint16_t*>(dq_), static_cast<uint16_t*>(dk_), static_cast<uint16_t*>(dv_), H,
-                       (int64_t)T * D, total, scale);
+                       static_cast<uint16_t*>(c.dq), static_cast<uint16_t*>(c.dk), static_cast<uint16_t*>(c.dv),
+                       c.dqs, c.dks, c.dvs, H, D, (int64_t)T * D, total, c.scale);
   return launch_status();
 }
 
@@ -2263,25 +2347,16 @@ int decode_entry(const DecCall& c) {
 
 template <class OP>
 int forward_entry(const FwdCall& c) {
-#define SA_FWD(DD)                                                                                                 \
-  return forward_impl<OP, DD>(c.q, c.k, c.v, c.out, c.rmax, c.rden, c.carry, c.state_in, c.state_out, c.state_ld, \
-                              c.ws, c.nseq, c.H, c.Tq, c.Tk, c.kvs, c.q_off, c.scale, c.exempt, c.group,           \
-                              c.damp_mode, c.train_len, c.st)
-  if (c.head_dim == 32) SA_FWD(32);
-  if (c.head_dim == 64) SA_FWD(64);
-  SA_FWD(128);
-#undef SA_FWD
+  if (c.head_dim == 32) return forward_impl<OP, 32>(c);
+  if (c.head_dim == 64) return forward_impl<OP, 64>(c);
+  return forward_impl<OP, 128>(c);
 }
 
 template <class OP>
 int backward_entry(const BwdCall& c) {
-#define SA_BWD(DD)                                                                                                 \
-  return backward_impl<OP, DD>(c.q, c.k, c.v, c.out, c.dout, c.rmax, c.rden, c.carry, c.dq, c.dk, c.dv, c.ws,    \
-                               c.nseq, c.H, c.T, c.scale, c.exempt, c.group, c.grad_dtype, c.st)
-  if (c.head_dim == 32) SA_BWD(32);
-  if (c.head_dim == 64) SA_BWD(64);
-  SA_BWD(128);
-#undef SA_BWD
+  if (c.head_dim == 32) return backward_impl<OP, 32>(c);
+  if (c.head_dim == 64) return backward_impl<OP, 64>(c);
+  return backward_impl<OP, 128>(c);
 }
 
 }  // namespace

@@ -1,7 +1,7 @@
 """Selective Attention (Leviathan, Kalman, Matias; ICLR 2025) on MI355X HIP kernels.
 
 Same exports as the reference package (reference src/selective_attention/__init__.py:3-17), plus
-the chunked-prefill and cached-decode entry points.
+the chunked-prefill, cached-decode and packed-projection entry points.
 """
 
 from .kernels import (
@@ -11,6 +11,7 @@ from .kernels import (
     selective_attention_decode,
     selective_attention_forward,
     selective_attention_prefill,
+    selective_attention_qkv,
     selective_attention_reference,
     selective_logits,
 )
@@ -22,6 +23,7 @@ __all__ = [
     "selective_attention_decode",
     "selective_attention_forward",
     "selective_attention_prefill",
+    "selective_attention_qkv",
     "selective_attention_reference",
     "selective_logits",
 ]

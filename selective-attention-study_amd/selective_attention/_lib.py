@@ -26,11 +26,18 @@ KERNEL_SELECTION = 2
 KERNEL_BACKWARD_DQ = 3
 KERNEL_DECODE = 4
 
+class ViewStrides(ctypes.Structure):
+    """sa_view_strides: element strides of a (sequence, head, row) view."""
+
+    _fields_ = [("seq", ctypes.c_int64), ("head", ctypes.c_int64), ("row", ctypes.c_int64)]
+
+
 # Every function the header declares, with its ctypes signature.
 _P = ctypes.c_void_p
 _I64 = ctypes.c_int64
 _I = ctypes.c_int
 _F = ctypes.c_float
+_VS = ctypes.POINTER(ViewStrides)
 SIGNATURES = {
     "sa_abi_version": (_I, []),
     "sa_status_string": (ctypes.c_char_p, [_I]),
@@ -40,7 +47,11 @@ SIGNATURES = {
     "sa_forward_workspace_bytes": (_I64, [_I64, _I64, _I64, _I64, _I]),
     "sa_forward": (_I, [_P, _P, _P, _P, _P, _P, _P, _P, _P, _I64, _P, _I64,
                         _I64, _I64, _I64, _I64, _I64, _I64, _I64, _F, _I, _I, _I, _I, _I64, _P]),
+    "sa_forward_strided": (_I, [_P, _VS, _P, _VS, _P, _VS, _P, _P, _VS, _P, _P, _P, _P, _P, _I64, _P, _I64,
+                                _I64, _I64, _I64, _I64, _I64, _I64, _F, _I, _I, _I, _I, _I64, _P]),
     "sa_backward_workspace_bytes": (_I64, [_I64, _I64, _I64, _I64, _I, _I]),
+    "sa_backward_strided": (_I, [_P, _VS, _P, _VS, _P, _VS, _P, _P, _VS, _P, _P, _P, _P, _VS, _P, _VS, _P, _VS,
+                                 _P, _I64, _I64, _I64, _I64, _I64, _F, _I, _I, _I, _I, _P]),
     "sa_backward": (_I, [_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _I64,
                          _I64, _I64, _I64, _I64, _F, _I, _I, _I, _I, _P]),
     "sa_decode_workspace_bytes": (_I64, [_I64, _I64, _I64, _I64]),

@@ -419,6 +419,114 @@ class _SelectiveAttentionFn(torch.autograd.Function):
         return grads + (None,) * 11
 
 
+class _SelectiveAttentionQKVFn(torch.autograd.Function):
+    """Layer-boundary fused form of the attention call: reads q, k, v straight out of the packed
+    projection (B, T, 3 * H * D) (the reference splits and transposes it, model.py:59-67), returns
+    the output as (B, T, H * D) in the projection's dtype (the reference's fp32 output, cast by
+    mixers.py:94, then transposed for c_proj), and writes the gradients straight into one
+    (B, T, 3 * H * D) tensor (no slice gradients to assemble). The arithmetic is that of
+    selective_attention: the same kernels through sa_forward_strided / sa_backward_strided."""
+
+    @staticmethod
+    def forward(ctx, qkv, heads, dot_precision, exempt):
+        batch, seq, c3 = qkv.shape
+        head_dim = c3 // (3 * heads)
+        dtype, es = _packed_layout(qkv, heads, dot_precision)
+        exempt = _check_exempt(exempt)
+        lib = _lib.load()
+        dev = qkv.device
+        cdim = heads * head_dim
+        n = batch * heads
+        nb = (seq + CARRY_M - 1) // CARRY_M
+        y = torch.empty(batch, seq, cdim, device=dev, dtype=qkv.dtype)
+        out = torch.empty(n, seq, head_dim, device=dev, dtype=torch.float32)
+        rmax = torch.empty(n, seq, device=dev, dtype=torch.float32)
+        rden = torch.empty(n, seq, device=dev, dtype=torch.float32)
+        carry = torch.empty(batch, nb, seq, device=dev, dtype=torch.float32)
+        state = torch.empty(batch, seq, device=dev, dtype=torch.float32)
+        ws = torch.empty(max(int(lib.sa_forward_workspace_bytes(batch, heads, seq, head_dim, dtype)), 1),
+                         device=dev, dtype=torch.uint8)
+        qkv_s = _lib.ViewStrides(seq * c3, head_dim, c3)
+        y_s = _lib.ViewStrides(seq * cdim, head_dim, cdim)
+        base = qkv.data_ptr()
+        with torch.cuda.device(dev):
+            _lib.check(lib.sa_forward_strided(
+                base, qkv_s, base + cdim * es, qkv_s, base + 2 * cdim * es, qkv_s, out.data_ptr(), y.data_ptr(),
+                y_s, rmax.data_ptr(), rden.data_ptr(), carry.data_ptr(), None, state.data_ptr(), state.stride(0),
+                ws.data_ptr(), ws.numel(), batch, heads, seq, seq, 0, head_dim, 1.0 / math.sqrt(head_dim), dtype,
+                exempt, 0, 0, 0, _stream(dev)))
+        ctx.save_for_backward(qkv, out, rmax, rden, carry)
+        ctx.meta = (dtype, es, exempt, heads, head_dim)
+        return y
+
+    @staticmethod
+    @once_differentiable
+    def backward(ctx, dy):
+        qkv, out, rmax, rden, carry = ctx.saved_tensors
+        dtype, es, exempt, heads, head_dim = ctx.meta
+        lib = _lib.load()
+        batch, seq, c3 = qkv.shape
+        cdim = heads * head_dim
+        dev = qkv.device
+        dy = dy.to(qkv.dtype).contiguous()
+        dqkv = torch.empty_like(qkv)
+        ws = torch.empty(int(lib.sa_backward_workspace_bytes(batch, heads, seq, head_dim, dtype, 0)), device=dev,
+                         dtype=torch.uint8)
+        qkv_s = _lib.ViewStrides(seq * c3, head_dim, c3)
+        dy_s = _lib.ViewStrides(seq * cdim, head_dim, cdim)
+        base, gbase = qkv.data_ptr(), dqkv.data_ptr()
+        with torch.cuda.device(dev):
+            _lib.check(lib.sa_backward_strided(
+                base, qkv_s, base + cdim * es, qkv_s, base + 2 * cdim * es, qkv_s, out.data_ptr(), dy.data_ptr(),
+                dy_s, rmax.data_ptr(), rden.data_ptr(), carry.data_ptr(), gbase, qkv_s, gbase + cdim * es, qkv_s,
+                gbase + 2 * cdim * es, qkv_s, ws.data_ptr(), ws.numel(), batch, heads, seq, head_dim,
+                1.0 / math.sqrt(head_dim), dtype, dtype, exempt, 0, _stream(dev)))
+        return dqkv, None, None, None
+
+
+def _packed_layout(qkv: torch.Tensor, heads: int, dot_precision: str | None) -> tuple[int, int]:
+    """(storage dtype code, element size) of a packed projection the fused form can read in place;
+    ValueError otherwise."""
+
+    if qkv.dim() != 3 or not qkv.is_cuda or qkv.shape[-1] % (3 * heads) != 0:
+        raise ValueError(f"qkv must be a CUDA (B, T, 3 * heads * D) tensor; got {tuple(qkv.shape)}, heads={heads}")
+    head_dim = qkv.shape[-1] // (3 * heads)
+    if head_dim not in (32, 64, 128):
+        raise ValueError(f"the packed form takes head_dim 32, 64 or 128; got {head_dim}")
+    dtype = _resolve_precision(dot_precision, qkv.dtype)
+    want = torch.bfloat16 if dtype == _lib.DTYPE_BF16 else torch.float32
+    if qkv.dtype != want:
+        raise ValueError(f"the packed form reads qkv in place: its dtype must be the operand dtype {want}; "
+                         f"got {qkv.dtype}")
+    if not qkv.is_contiguous() or qkv.data_ptr() % 16:
+        raise ValueError("qkv must be contiguous and 16-byte aligned")
+    if not HAS_HIP:
+        _lib.load()   # raises RuntimeError with the reason
+    return dtype, qkv.element_size()
+
+
+def packed_supported(qkv: torch.Tensor, heads: int, dot_precision: str | None = None) -> bool:
+    """True when selective_attention_qkv can read this projection in place."""
+
+    try:
+        _packed_layout(qkv, heads, dot_precision)
+    except (ValueError, RuntimeError):
+        return False
+    return True
+
+
+def selective_attention_qkv(qkv: torch.Tensor, heads: int, dot_precision: str | None = None,
+                            exempt: int = 1) -> torch.Tensor:
+    """Differentiable Selective Attention on a packed projection: qkv (B, T, 3 * heads * D), laid out
+    as (B, T, 3, heads, D) like the reference's c_attn output (model.py:59-67), read in place; returns
+    (B, T, heads * D) in qkv's dtype, the layout the output projection reads. Equal to
+    selective_attention on the split heads with the output cast to qkv's dtype and merged
+    (mixers.py:94, model.py:69-71). qkv's dtype must be the operand dtype (bf16, or fp32 under
+    dot_precision "tf32" or "ieee"); see packed_supported."""
+
+    return _SelectiveAttentionQKVFn.apply(qkv, int(heads), dot_precision, exempt)
+
+
 def selective_attention(
     q: torch.Tensor,
     k: torch.Tensor,

@@ -99,7 +99,18 @@ def selective_class():
 
             def forward(self, x: Tensor) -> Tensor:
                 b, t, _ = x.shape
-                q, k, v = self._split_heads(x)
+                qkv = self.c_attn(x)
+                if (self.use_kernel and self.groups == 1 and self.history_damp in (None, "none")
+                        and kernels.packed_supported(qkv, self.n_heads, self.dot_precision)):
+                    # layer-boundary fused form: q, k, v read in place from the projection, the
+                    # output written in the layout c_proj reads, the gradient as one tensor
+                    if self.training and self.dropout > 0.0:
+                        raise RuntimeError("selective attention kernels have no attention dropout; set dropout=0")
+                    y = kernels.selective_attention_qkv(qkv, self.n_heads, self.dot_precision, self.exempt)
+                    return self.resid_dropout(self.c_proj(y))
+                hd = self.d_model // self.n_heads
+                qkv = qkv.view(b, t, 3, self.n_heads, hd)
+                q, k, v = (qkv[:, :, i].transpose(1, 2) for i in range(3))
                 return self._merge_heads(self._attend(q, k, v)[0], b, t)
 
             # -- cached generation ---------------------------------------------------------------

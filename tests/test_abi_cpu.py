@@ -111,6 +111,34 @@ def test_invalid_arguments_are_rejected_before_any_launch():
     assert lib.sa_backward(*bad) == -3
 
 
+def test_strided_views_are_validated_before_any_launch():
+    """sa_forward_strided / sa_backward_strided check every view (no pointer dereferenced)."""
+    lib = _lib.load()
+    fake = 1 << 20
+    V = _lib.ViewStrides
+    good = V(16 * 3 * 4 * 64, 64, 3 * 4 * 64)   # a packed (B, T=16, 3, H=4, 64) projection
+    ws = 1 << 30
+
+    def fwd(qs=good, ks=good, vs=good, y=None, ys=None, q=fake):
+        return lib.sa_forward_strided(q, qs, fake + 512, ks, fake + 1024, vs, fake, y, ys, fake, fake, fake, None,
+                                      fake, 16, fake, ws, 1, 4, 16, 16, 0, 64, 0.125, 0, 1, 0, 0, 0, None)
+
+    assert fwd(qs=V(0, 64, 32)) == -1                     # row stride below head_dim
+    assert fwd(ks=V(16 * 768, 64, 770)) == -1             # row stride not a multiple of 8 elements
+    assert fwd(q=fake + 8) == -1                          # pointer not 16-byte aligned
+    assert fwd(y=fake, ys=V(16 * 256, 32, 256)) == -1     # output heads overlap
+    assert fwd(y=fake, ys=None) == -1                     # output without a view
+    assert fwd(qs=V(16 * 768, 64, 1 << 27)) == -1         # rows past the 2 GiB a head may span
+
+    def bwd(dqs=good, dos=good):
+        return lib.sa_backward_strided(fake, good, fake, good, fake, good, fake, fake, dos, fake, fake, fake,
+                                       fake, dqs, fake, good, fake, good, fake, ws, 1, 4, 16, 64, 0.125, 0, 0, 1,
+                                       0, None)
+
+    assert bwd(dqs=V(0, 16, 768)) == -1                   # gradient heads overlap
+    assert bwd(dos=V(0, 64, 60)) == -1                    # dout row stride below head_dim
+
+
 def test_api_checks_on_cpu_tensors():
     q = torch.randn(1, 2, 16, 32)
     assert not kernels.supported(q)
