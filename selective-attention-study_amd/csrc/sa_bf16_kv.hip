@@ -1,0 +1,23 @@
+// The key-side backward kernel's bf16-storage instances, in a translation unit of their own:
+// build.sh compiles it with the compiler's iterative ILP scheduler (and the MFMA accumulators in
+// VGPRs, as sa_bf16.hip), which measures faster for this kernel and slower for the others.
+
+#include "sa_kernels.h"
+
+namespace sa_host {
+
+int launch_bwd_kv_bf16(int D, int G, bool cv, const KvLaunch& a) {
+#define SA_KV(DD, GG)                                        \
+  if (cv) launch_kv_from<OpBF16, DD, GG, true>(a);           \
+  else launch_kv_from<OpBF16, DD, GG, false>(a);             \
+  return launch_status()
+  if (D == 32) {
+    if (G == 2) { SA_KV(32, 2); }
+    SA_KV(32, 1);
+  }
+  if (D == 64) { SA_KV(64, 1); }
+  SA_KV(128, 1);
+#undef SA_KV
+}
+
+}  // namespace sa_host

@@ -205,6 +205,20 @@ inline int64_t decode_workspace_bytes(int64_t nseq, int64_t heads, int64_t t, in
   return align_up((decode_partials_floats(nseq, heads, t, D) + nseq * heads * t) * 4, 256);
 }
 
+// The key-side backward kernel's arguments, for a launch from another translation unit.
+struct KvLaunch {
+  const void *q, *k, *v, *qt, *dout, *dot;
+  Strides qs, ks, vs, dos;
+  const float *lse, *dbar, *carry;
+  float *ucheck, *dk, *dv, *dk0x;
+  int nseq, H, T;
+  int64_t ldt;
+  int exempt;
+  float scale;
+  hipStream_t st;
+};
+SA_HIDDEN int launch_bwd_kv_bf16(int D, int G, bool cv, const KvLaunch& a);   // sa_bf16_kv.hip
+
 SA_HIDDEN int forward_bf16(const FwdCall& c);    // sa_bf16.hip
 SA_HIDDEN int backward_bf16(const BwdCall& c);
 SA_HIDDEN int forward_f32(const FwdCall& c);     // sa_f32.hip

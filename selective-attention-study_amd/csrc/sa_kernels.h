@@ -2203,6 +2203,17 @@ int forward_impl(const FwdCall& c) {
   return launch_status();
 }
 
+// Launch of the key-side kernel from its arguments (the grid as launch_bwd's).
+template <class OP, int D, int G, bool CV>
+void launch_kv_from(const KvLaunch& a) {
+  using elem = typename OP::elem;
+  dim3 grid((unsigned)cdiv(a.T, NWAVES * TILE), (unsigned)(a.nseq * (a.H / G)));
+  hipLaunchKernelGGL((bwd_kv_kernel<OP, D, G, CV>), grid, dim3(NTHREADS), 0, a.st, static_cast<const elem*>(a.q),
+                     static_cast<const elem*>(a.k), static_cast<const elem*>(a.v), static_cast<const elem*>(a.qt),
+                     static_cast<const elem*>(a.dout), static_cast<const elem*>(a.dot), a.qs, a.ks, a.vs, a.dos, a.lse,
+                     a.dbar, a.carry, a.ucheck, a.dk, a.dv, a.dk0x, a.nseq, a.H, a.T, a.ldt, a.exempt, a.scale);
+}
+
 template <class OP, int D, int G>
 void launch_bwd(const BwdCall& c, const typename OP::elem* qt, const typename OP::elem* kt,
                 const typename OP::elem* dot, const float* lse, const float* dbar, float* ucheck, float* dq,
@@ -2218,10 +2229,16 @@ void launch_bwd(const BwdCall& c, const typename OP::elem* qt, const typename OP
     return s.row == D && s.head == (int64_t)c.T * D && s.seq == (int64_t)c.H * s.head;
   };
   const bool cv = contiguous(c.qs) && contiguous(c.ks) && contiguous(c.vs) && contiguous(c.dos);
+  // bf16: the key-side kernel lives in its own translation unit (sa_bf16_kv.hip), built with the
+  // compiler's iterative ILP scheduler, which measures faster for it (and slower for the others)
+  const KvLaunch kv{q,     k,     v,       qt,      dout,     dot,    c.qs,   c.ks,     c.vs,  c.dos,  lse,
+                    dbar,  c.carry, ucheck, dk,      dv,       dk0x,   c.nseq, c.H,      c.T,   ldt,    c.exempt,
+                    c.scale, c.st};
 #define SA_LAUNCH_KV(CVV)                                                                                         \
-  hipLaunchKernelGGL((bwd_kv_kernel<OP, D, G, CVV>), grid, dim3(NTHREADS), 0, c.st, q, k, v, qt, dout, dot, c.qs, \
-                     c.ks, c.vs, c.dos, lse, dbar, c.carry, ucheck, dk, dv, dk0x, c.nseq, c.H, c.T, ldt, c.exempt,  \
-                     c.scale)
+  do {                                                                                                            \
+    if constexpr (sizeof(elem) == 2) launch_bwd_kv_bf16(D, G, CVV, kv);                                          \
+    else launch_kv_from<OP, D, G, CVV>(kv);                                                                       \
+  } while (0)
 #define SA_LAUNCH_DQ(CVV)                                                                                         \
   hipLaunchKernelGGL((bwd_dq_kernel<OP, D, G, CVV>), grid, dim3(NTHREADS), 0, c.st, q, k, v, kt, dout, c.qs, c.ks, \
                      c.vs, c.dos, lse, dbar, c.carry, ucheck, dq, dq0x, c.nseq, c.H, c.T, ldt, c.exempt, c.scale)
