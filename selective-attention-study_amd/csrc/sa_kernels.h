@@ -724,18 +724,22 @@ __global__ __launch_bounds__(NTHREADS, (fwd_min_blocks<OP, D, G>())) void fwd_ke
   store_tile(0);
   __syncthreads();
 
-  for (int t = 0; t < wg_end; ++t) {
+  // one key tile; INTERIOR: every key of the tile strictly precedes every query of the workgroup,
+  // lies before the end and is not exempt, for every wavefront (straight-line code without masks)
+  auto tile_step = [&](int t, auto interior_tag) {
+    constexpr bool INTERIOR = decltype(interior_tag)::value;
     const int kt = wg_end - 1 - t;
     const int buf = NBUF == 2 ? (t & 1) : 0;
     if (t + 1 < wg_end) load_tile(kt - 1);
-    if (kt < my_end) {
+    if (kt < my_end) {   // (a wavefront past the last query block has none)
       const int kbase = kt * TILE;
       // edge: some key of the tile does not strictly precede every query of the block, lies past
       // the end or is exempt; interior tiles skip the masks (the selection gate is then the logit's
       // sign alone)
-      const bool edge = (kbase + TILE - 1 >= q_off + rb * TILE) || (kbase + TILE > Tk) || kbase < exempt;
-      // (one body for both kinds of tile: two copies of its accumulating products would make the
-      // compiler copy the output sums between register sets every tile)
+      const bool edge =
+          !INTERIOR && ((kbase + TILE - 1 >= q_off + rb * TILE) || (kbase + TILE > Tk) || kbase < exempt);
+      // (one body for both kinds of tile within a loop: two copies of its accumulating products
+      // would make the compiler copy the output sums between register sets every tile)
       auto body = [&]() {
         // Head 0's logits as (queries x keys), lane = key kbase + n: the selection's running sum
         // over queries then stays within the lane. -F (logit units) = -(the carry at the block's
@@ -838,7 +842,15 @@ __global__ __launch_bounds__(NTHREADS, (fwd_min_blocks<OP, D, G>())) void fwd_ke
     if constexpr (NBUF == 1) __syncthreads();   // the one buffer is free again
     if (t + 1 < wg_end) store_tile(NBUF == 2 ? buf ^ 1 : 0);
     __syncthreads();
-  }
+  };
+  // key tiles newest first: the diagonals and the sequence end, the interior tiles
+  // [i_lo, i_hi), then the tiles holding exempt keys
+  const int i_lo = min((exempt + TILE - 1) / TILE, wg_end);
+  const int i_hi = max(i_lo, min(min(q_off + qsb * NWAVES * TILE, Tk) / TILE, wg_end));
+  int t = 0;
+  for (; t < wg_end - i_hi; ++t) tile_step(t, std::false_type{});
+  for (; t < wg_end - i_lo; ++t) tile_step(t, std::true_type{});
+  for (; t < wg_end; ++t) tile_step(t, std::false_type{});
 
   if (rb >= NBq || q_rel >= Tq) return;
 #pragma unroll
@@ -1335,7 +1347,10 @@ __global__ __launch_bounds__(NTHREADS, (kv_min_blocks<OP, D, G>())) void bwd_kv_
       __syncthreads();
     }
 
-    for (int t = 0; t < ntiles; ++t) {
+    // one query tile; INTERIOR: every pair of the tile is unmasked for every wavefront and no key
+    // is exempt, so the body is straight-line code without the masks and split products
+    auto tile_step = [&](int t, auto interior_tag) {
+      constexpr bool INTERIOR = decltype(interior_tag)::value;
       const int qb = NB - 1 - t;
       const int qbase = qb * TILE;
       const int buf = NBUF == 2 ? (t & 1) : 0;
@@ -1353,12 +1368,13 @@ __global__ __launch_bounds__(NTHREADS, (kv_min_blocks<OP, D, G>())) void bwd_kv_
         store_tile(0);
         __syncthreads();
       }
-      if (qbase + TILE - 1 >= key0) {   // else every query of the tile precedes every key
+      if (INTERIOR || qbase + TILE - 1 >= key0) {   // else every query of the tile precedes every key
         if (h == 0 && j < T) uplane[(int64_t)qb * T + j] = ucarry;
         // tile body; edge: some pair of the tile is masked (diagonal, sequence end) or exempt
         // (rows past the end and keys past the end need no mask on the key side: the latter's sums
         // stay in their own lanes, which are never written)
-        const bool edge = (qbase <= key0 + TILE - 1) || key0 < exempt;
+        const bool edge = !INTERIOR && ((qbase <= key0 + TILE - 1) || key0 < exempt);
+        const bool split = !INTERIOR && split_keys;
         const TileMasks mk(j, qbase, T, exempt, h);
         // (a lambda: inlined late, its loop-invariant parts are not hoisted out of the tile loop,
         // which would hold them in registers across it)
@@ -1390,7 +1406,7 @@ __global__ __launch_bounds__(NTHREADS, (kv_min_blocks<OP, D, G>())) void bwd_kv_
             for (int s = 0; s < NS; ++s) dp = OP::mma(OP::ld_std(sdO[buf][g], LDK, n, h, s), v_frag(g, s), dp);
             f32x16 pr, dz;
             p_dz_tile<false>(lg, dp, sLse[buf][g], sl2, h, edge, mk, pr, dz);
-            acc_t(dvt[g], sdOt[buf][g], pr, split_keys);
+            acc_t(dvt[g], sdOt[buf][g], pr, split);
             if (g == 0) {
               dzsum = dz;
             } else {
@@ -1398,7 +1414,7 @@ __global__ __launch_bounds__(NTHREADS, (kv_min_blocks<OP, D, G>())) void bwd_kv_
               for (int i = 0; i < 16; ++i) dzsum[i] += dz[i];
             }
             if (H0 && g == 0) dz0 = dz;   // head 0's dK waits for g
-            else acc_t(dkt[g], sQt[buf][g], dz, split_keys);
+            else acc_t(dkt[g], sQt[buf][g], dz, split);
           }
           f32x16 gp;
           ucarry = gpath_tile(dzsum, ucarry, gate, h, gp);
@@ -1417,7 +1433,12 @@ __global__ __launch_bounds__(NTHREADS, (kv_min_blocks<OP, D, G>())) void bwd_kv_
         if (t + 1 < ntiles) store_tile(NBUF == 2 ? buf ^ 1 : 0);
         __syncthreads();
       }
-    }
+    };
+    // The last NWAVES tiles hold the wavefronts' diagonals; a workgroup with an exempt key runs
+    // every tile with the masks.
+    const int n_int = (qb_lo * TILE < exempt) ? 0 : max(ntiles - NWAVES, 0);
+    for (int t = 0; t < n_int; ++t) tile_step(t, std::true_type{});
+    for (int t = n_int; t < ntiles; ++t) tile_step(t, std::false_type{});
   };
   if (has_h0) sweep(std::true_type{});
   else sweep(std::false_type{});
@@ -1700,6 +1721,8 @@ __global__ __launch_bounds__(NTHREADS, (dq_min_blocks<OP, D>())) void bwd_dq_ker
       __syncthreads();
     }
 
+    // (one loop for edge and interior tiles: split into an interior loop without the masks, the
+    // query side measured slower, unlike the forward and the key side)
     for (int ktile = 0; ktile < wg_end; ++ktile) {
       const int kbase = ktile * TILE;
       const int buf = NBUF == 2 ? (ktile & 1) : 0;
