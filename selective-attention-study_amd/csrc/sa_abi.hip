@@ -190,7 +190,9 @@ int sa_backward_strided(const void* q, const sa_view_strides* q_strides, const v
       !view_ok(dq_strides, t, head_dim, grad_dtype, true) || !view_ok(dk_strides, t, head_dim, grad_dtype, true) ||
       !view_ok(dv_strides, t, head_dim, grad_dtype, true))
     return SA_ERR_ARGUMENT;
-  if (((uintptr_t)q | (uintptr_t)k | (uintptr_t)v | (uintptr_t)dout) % 16) return SA_ERR_ARGUMENT;
+  if (((uintptr_t)q | (uintptr_t)k | (uintptr_t)v | (uintptr_t)dout | (uintptr_t)dq | (uintptr_t)dk | (uintptr_t)dv) %
+      16)
+    return SA_ERR_ARGUMENT;
   if (group < 0 || workspace_bytes < sa_backward_workspace_bytes(nseq, heads, t, head_dim, dtype, group))
     return SA_ERR_WORKSPACE;
   auto st = [](const sa_view_strides* p) { return Strides{p->seq, p->head, (int)p->row}; };

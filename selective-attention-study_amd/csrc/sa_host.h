@@ -99,11 +99,12 @@ inline int bwd_group(int dtype, int64_t D, int64_t heads, int requested) {
 }
 
 struct BwdLayout {
-  int64_t qt, dot, kt, lse, dbar, dq, dk, dv, dq0x, dk0x, ucheck, total;
+  int64_t qt, dot, kt, lse, dbar, dq, dk, dq0x, dk0x, ucheck, total;
 };
 
-// Workspace of sa_backward: transposed Q, dO, K; row statistics; fp32 gradient sums; head 0's
-// shares from other groups; the selection-suffix checkpoints (one plane per head group).
+// Workspace of sa_backward: transposed Q, dO, K; row statistics; head 0's fp32 dQ, dK sums and
+// its shares from the other groups (every other gradient goes straight to the caller's views);
+// the selection-suffix checkpoints (one plane per head group).
 inline BwdLayout bwd_layout(int64_t nseq, int64_t heads, int64_t t, int64_t D, int64_t esize, int64_t G) {
   const int64_t R = nseq * heads, ldt = sa_transposed_ld(t), NB = (t + TILE - 1) / TILE;
   BwdLayout L;
@@ -114,9 +115,8 @@ inline BwdLayout bwd_layout(int64_t nseq, int64_t heads, int64_t t, int64_t D, i
   L.kt = take(R * D * ldt * esize);
   L.lse = take(R * t * 4);
   L.dbar = take(R * t * 4);
-  L.dq = take(R * t * D * 4);
-  L.dk = take(R * t * D * 4);
-  L.dv = take(R * t * D * 4);
+  L.dq = take(nseq * t * D * 4);   // head 0's own fp32 sums (the other heads write their views)
+  L.dk = take(nseq * t * D * 4);
   L.dq0x = take(nseq * t * D * 4);
   L.dk0x = take(nseq * t * D * 4);
   L.ucheck = take((heads / G) * nseq * NB * t * 4);
@@ -144,6 +144,13 @@ struct Strides {
   int64_t seq, head;
   int row;
   __host__ __device__ int64_t at(int64_t b, int64_t h) const { return b * seq + h * head; }
+};
+
+// A gradient output view: element type fp32 (f32) or bf16, (sequence, head, row) strides.
+struct GradView {
+  void* p;
+  Strides s;
+  int f32;
 };
 
 // One sa_forward call after its checks (pointers already typed by the storage dtype's entry).
@@ -210,7 +217,8 @@ struct KvLaunch {
   const void *q, *k, *v, *qt, *dout, *dot;
   Strides qs, ks, vs, dos;
   const float *lse, *dbar, *carry;
-  float *ucheck, *dk, *dv, *dk0x;
+  float *ucheck, *dk0h, *dk0x;
+  GradView dkv, dvv;
   int nseq, H, T;
   int64_t ldt;
   int exempt;

@@ -996,6 +996,25 @@ template <class OP, int D, int G>
 constexpr int kv_min_blocks() { return (sizeof(typename OP::elem) == 2 && D <= 64 && G == 1) ? SA_KV_MIN_BLOCKS : 1; }
 
 // ---------------------------------------------------------------------------------------------
+// Gradient stores to a caller's view (fp32 or bf16 elements): one element, or four consecutive
+// elements of a row (d a multiple of 4; the views' rows start 16-byte aligned).
+__device__ __forceinline__ void store_grad1(const GradView& v, int64_t b, int hh, int row, int d, float x) {
+  const int64_t o = v.s.at(b, hh) + (int64_t)row * v.s.row + d;
+  if (v.f32) static_cast<float*>(v.p)[o] = x;
+  else static_cast<uint16_t*>(v.p)[o] = OpBF16::to_elem(x);
+}
+__device__ __forceinline__ void store_grad4(const GradView& v, int64_t b, int hh, int row, int d, float4 x) {
+  const int64_t o = v.s.at(b, hh) + (int64_t)row * v.s.row + d;
+  if (v.f32) {
+    *reinterpret_cast<float4*>(static_cast<float*>(v.p) + o) = x;
+  } else {
+    *reinterpret_cast<uint2*>(static_cast<uint16_t*>(v.p) + o) =
+        make_uint2((uint32_t)OpBF16::to_elem(x.x) | ((uint32_t)OpBF16::to_elem(x.y) << 16),
+                   (uint32_t)OpBF16::to_elem(x.z) | ((uint32_t)OpBF16::to_elem(x.w) << 16));
+  }
+}
+
+// ---------------------------------------------------------------------------------------------
 // Backward helpers on (queries x keys) C-layout tiles: lane n holds key j = key0 + n, rows are the
 // queries qbase + crow(i, h), i = 0..15 (h = lane / 32).
 
@@ -1129,8 +1148,8 @@ __global__ __launch_bounds__(NTHREADS, (kv_min_blocks<OP, D, G>())) void bwd_kv_
     const typename OP::elem* __restrict__ v, const typename OP::elem* __restrict__ qt,
     const typename OP::elem* __restrict__ dout, const typename OP::elem* __restrict__ dot, Strides qs,
     Strides ks, Strides vs, Strides dos, const float* __restrict__ lse, const float* __restrict__ dbar,
-    const float* __restrict__ carry, float* __restrict__ ucheck, float* __restrict__ dk, float* __restrict__ dv,
-    float* __restrict__ dk0x, int nseq, int H, int T, int64_t ldt, int exempt, float scale) {
+    const float* __restrict__ carry, float* __restrict__ ucheck, float* __restrict__ dk0h, float* __restrict__ dk0x,
+    GradView dkv, GradView dvv, int nseq, int H, int T, int64_t ldt, int exempt, float scale) {
   using elem = typename OP::elem;
   using frag = typename OP::frag;
   constexpr int NS = D / OP::KS;
@@ -1444,21 +1463,22 @@ __global__ __launch_bounds__(NTHREADS, (kv_min_blocks<OP, D, G>())) void bwd_kv_
   else sweep(std::false_type{});
 
   if (j >= T) return;
+  // dV of every head and dK of heads other than 0 go to the caller's views; head 0's dK to its
+  // fp32 sums, where the other groups' shares join it
 #pragma unroll
   for (int g = 0; g < G; ++g) {
-    const int64_t row = seq_row + hd0 + g;
-    float* dkr = dk + (row * T + j) * D;
-    float* dvr = dv + (row * T + j) * D;
+    const int hh = hd0 + g;
 #pragma unroll
     for (int db = 0; db < DB; ++db)
 #pragma unroll
       for (int a = 0; a < 4; ++a) {
         const int d = db * 32 + 8 * a + 4 * h;
-        *reinterpret_cast<float4*>(dkr + d) =
-            make_float4(dkt[g][db][4 * a] * scale, dkt[g][db][4 * a + 1] * scale,
-                        dkt[g][db][4 * a + 2] * scale, dkt[g][db][4 * a + 3] * scale);
-        *reinterpret_cast<float4*>(dvr + d) =
-            make_float4(dvt[g][db][4 * a], dvt[g][db][4 * a + 1], dvt[g][db][4 * a + 2], dvt[g][db][4 * a + 3]);
+        const float4 kq = make_float4(dkt[g][db][4 * a] * scale, dkt[g][db][4 * a + 1] * scale,
+                                      dkt[g][db][4 * a + 2] * scale, dkt[g][db][4 * a + 3] * scale);
+        store_grad4(dvv, b, hh, j, d,
+                    make_float4(dvt[g][db][4 * a], dvt[g][db][4 * a + 1], dvt[g][db][4 * a + 2], dvt[g][db][4 * a + 3]));
+        if (hh == 0) *reinterpret_cast<float4*>(dk0h + ((int64_t)b * T + j) * D + d) = kq;
+        else store_grad4(dkv, b, hh, j, d, kq);
       }
   }
   if (!has_h0) {
@@ -1484,8 +1504,8 @@ __global__ __launch_bounds__(NTHREADS, (dq_min_blocks<OP, D>())) void bwd_dq_ker
     const typename OP::elem* __restrict__ v, const typename OP::elem* __restrict__ kt,
     const typename OP::elem* __restrict__ dout, Strides qs, Strides ks, Strides vs, Strides dos,
     const float* __restrict__ lse, const float* __restrict__ dbar, const float* __restrict__ carry,
-    const float* __restrict__ ucheck, float* __restrict__ dq, float* __restrict__ dq0x, int nseq, int H, int T,
-    int64_t ldt, int exempt, float scale) {
+    const float* __restrict__ ucheck, float* __restrict__ dq0h, float* __restrict__ dq0x, GradView dqv, int nseq,
+    int H, int T, int64_t ldt, int exempt, float scale) {
   using elem = typename OP::elem;
   using frag = typename OP::frag;
   constexpr int NS = D / OP::KS;
@@ -1811,15 +1831,20 @@ __global__ __launch_bounds__(NTHREADS, (dq_min_blocks<OP, D>())) void bwd_dq_ker
   else sweep(std::false_type{});
 
   if (qb >= NB) return;
+  // heads other than 0: dQ (scaled) to the caller's view; head 0: unscaled fp32 sums, where the
+  // other groups' shares join it
 #pragma unroll
   for (int g = 0; g < G; ++g) {
-    const int64_t row = seq_row + hd0 + g;
+    const int hh = hd0 + g;
 #pragma unroll
     for (int i = 0; i < 16; ++i) {
       const int r = qbase + crow(i, h);
       if (r < T) {
 #pragma unroll
-        for (int db = 0; db < DB; ++db) dq[(row * T + r) * D + db * 32 + n] = dqacc[g][db][i];
+        for (int db = 0; db < DB; ++db) {
+          if (hh == 0) dq0h[((int64_t)b * T + r) * D + db * 32 + n] = dqacc[g][db][i];
+          else store_grad1(dqv, b, hh, r, db * 32 + n, dqacc[g][db][i] * scale);
+        }
       }
     }
   }
@@ -1837,29 +1862,19 @@ __global__ __launch_bounds__(NTHREADS, (dq_min_blocks<OP, D>())) void bwd_dq_ker
 
 // Gradients to the output dtype (bf16 or fp32): dq*scale, dk, dv, with head 0's dQ and dK shares
 // from the other head groups (dq0x unscaled, dk0x scaled) added to head 0.
-__device__ __forceinline__ void store_grad(uint16_t* p, float x) { *p = OpBF16::to_elem(x); }
-__device__ __forceinline__ void store_grad(float* p, float x) { *p = x; }
 
-// The fp32 sums are (b * H + head, t, D) contiguous; the outputs are views (Strides).
-template <typename OUT>
+// Head 0's gradients: its own fp32 sums plus the other groups' shares, (b, t, D) contiguous, four
+// elements per thread, to the caller's views.
 __global__ __launch_bounds__(NTHREADS) void bwd_finish_kernel(
-    const float* __restrict__ dq32, const float* __restrict__ dk32, const float* __restrict__ dv32,
-    const float* __restrict__ dq0x, const float* __restrict__ dk0x, OUT* __restrict__ dq, OUT* __restrict__ dk,
-    OUT* __restrict__ dv, Strides dqs, Strides dks, Strides dvs, int H, int D, int64_t TD, int64_t total,
-    float scale) {
-  for (int64_t e = (int64_t)blockIdx.x * NTHREADS + threadIdx.x; e < total; e += (int64_t)gridDim.x * NTHREADS) {
-    const int64_t row = e / TD;          // b*H + head
-    const int64_t off = e - row * TD;
-    const int64_t b = row / H, hd = row - b * H;
-    const int64_t t = off / D, d = off - t * D;
-    float qv = dq32[e], kv = dk32[e];
-    if (hd == 0) {
-      qv += dq0x[b * TD + off];
-      kv += dk0x[b * TD + off];
-    }
-    store_grad(dq + dqs.at(b, hd) + t * dqs.row + d, qv * scale);
-    store_grad(dk + dks.at(b, hd) + t * dks.row + d, kv);
-    store_grad(dv + dvs.at(b, hd) + t * dvs.row + d, dv32[e]);
+    const float4* __restrict__ dq0h, const float4* __restrict__ dk0h, const float4* __restrict__ dq0x,
+    const float4* __restrict__ dk0x, GradView dqv, GradView dkv, int D, int64_t TD, int64_t total4, float scale) {
+  for (int64_t e = (int64_t)blockIdx.x * NTHREADS + threadIdx.x; e < total4; e += (int64_t)gridDim.x * NTHREADS) {
+    const int64_t b = (4 * e) / TD, off = 4 * e - b * TD;
+    const int t = (int)(off / D), d = (int)(off - (int64_t)t * D);
+    const float4 q = dq0h[e], qx = dq0x[e], k = dk0h[e], kx = dk0x[e];
+    store_grad4(dqv, b, 0, t, d, make_float4((q.x + qx.x) * scale, (q.y + qx.y) * scale, (q.z + qx.z) * scale,
+                                             (q.w + qx.w) * scale));
+    store_grad4(dkv, b, 0, t, d, make_float4(k.x + kx.x, k.y + kx.y, k.z + kx.z, k.w + kx.w));
   }
 }
 
@@ -2234,13 +2249,14 @@ void launch_kv_from(const KvLaunch& a) {
   hipLaunchKernelGGL((bwd_kv_kernel<OP, D, G, CV>), grid, dim3(NTHREADS), 0, a.st, static_cast<const elem*>(a.q),
                      static_cast<const elem*>(a.k), static_cast<const elem*>(a.v), static_cast<const elem*>(a.qt),
                      static_cast<const elem*>(a.dout), static_cast<const elem*>(a.dot), a.qs, a.ks, a.vs, a.dos, a.lse,
-                     a.dbar, a.carry, a.ucheck, a.dk, a.dv, a.dk0x, a.nseq, a.H, a.T, a.ldt, a.exempt, a.scale);
+                     a.dbar, a.carry, a.ucheck, a.dk0h, a.dk0x, a.dkv, a.dvv, a.nseq, a.H, a.T, a.ldt, a.exempt,
+                     a.scale);
 }
 
 template <class OP, int D, int G>
 void launch_bwd(const BwdCall& c, const typename OP::elem* qt, const typename OP::elem* kt,
-                const typename OP::elem* dot, const float* lse, const float* dbar, float* ucheck, float* dq,
-                float* dk, float* dv, float* dq0x, float* dk0x, int64_t ldt) {
+                const typename OP::elem* dot, const float* lse, const float* dbar, float* ucheck, float* dq0h,
+                float* dk0h, float* dq0x, float* dk0x, int64_t ldt) {
   using elem = typename OP::elem;
   const elem* q = static_cast<const elem*>(c.q);
   const elem* k = static_cast<const elem*>(c.k);
@@ -2254,9 +2270,11 @@ void launch_bwd(const BwdCall& c, const typename OP::elem* qt, const typename OP
   const bool cv = contiguous(c.qs) && contiguous(c.ks) && contiguous(c.vs) && contiguous(c.dos);
   // bf16: the key-side kernel lives in its own translation unit (sa_bf16_kv.hip), built with the
   // compiler's iterative ILP scheduler, which measures faster for it (and slower for the others)
-  const KvLaunch kv{q,     k,     v,       qt,      dout,     dot,    c.qs,   c.ks,     c.vs,  c.dos,  lse,
-                    dbar,  c.carry, ucheck, dk,      dv,       dk0x,   c.nseq, c.H,      c.T,   ldt,    c.exempt,
-                    c.scale, c.st};
+  const int f32 = c.grad_dtype == SA_DTYPE_F32;
+  const GradView dqv{c.dq, c.dqs, f32}, dkv{c.dk, c.dks, f32}, dvv{c.dv, c.dvs, f32};
+  const KvLaunch kv{q,    k,       v,      qt,   dout, dot,    c.qs, c.ks, c.vs, c.dos,    lse,      dbar,
+                    c.carry, ucheck, dk0h, dk0x, dkv,  dvv,    c.nseq, c.H,  c.T,  ldt,      c.exempt, c.scale,
+                    c.st};
 #define SA_LAUNCH_KV(CVV)                                                                                         \
   do {                                                                                                            \
     if constexpr (sizeof(elem) == 2) launch_bwd_kv_bf16(D, G, CVV, kv);                                          \
@@ -2264,7 +2282,8 @@ void launch_bwd(const BwdCall& c, const typename OP::elem* qt, const typename OP
   } while (0)
 #define SA_LAUNCH_DQ(CVV)                                                                                         \
   hipLaunchKernelGGL((bwd_dq_kernel<OP, D, G, CVV>), grid, dim3(NTHREADS), 0, c.st, q, k, v, kt, dout, c.qs, c.ks, \
-                     c.vs, c.dos, lse, dbar, c.carry, ucheck, dq, dq0x, c.nseq, c.H, c.T, ldt, c.exempt, c.scale)
+                     c.vs, c.dos, lse, dbar, c.carry, ucheck, dq0h, dq0x, dqv, c.nseq, c.H, c.T, ldt, c.exempt,   \
+                     c.scale)
   {
     TimedLaunch timed(SA_KERNEL_BACKWARD, c.st);
     if (cv) SA_LAUNCH_KV(true);
@@ -2294,9 +2313,8 @@ int backward_impl(const BwdCall& c) {
   elem* kt = reinterpret_cast<elem*>(base + L.kt);
   float* lse = reinterpret_cast<float*>(base + L.lse);
   float* dbar = reinterpret_cast<float*>(base + L.dbar);
-  float* dq32 = reinterpret_cast<float*>(base + L.dq);
-  float* dk32 = reinterpret_cast<float*>(base + L.dk);
-  float* dv32 = reinterpret_cast<float*>(base + L.dv);
+  float* dq0h = reinterpret_cast<float*>(base + L.dq);
+  float* dk0h = reinterpret_cast<float*>(base + L.dk);
   float* dq0x = reinterpret_cast<float*>(base + L.dq0x);
   float* dk0x = reinterpret_cast<float*>(base + L.dk0x);
   float* ucheck = reinterpret_cast<float*>(base + L.ucheck);
@@ -2315,7 +2333,7 @@ int backward_impl(const BwdCall& c) {
                      (int64_t)((int64_t)nseq * T * D / 4));
   hipLaunchKernelGGL(fill_zero_kernel, dim3(256), dim3(NTHREADS), 0, st, reinterpret_cast<float4*>(dk0x),
                      (int64_t)((int64_t)nseq * T * D / 4));
-#define SA_LAUNCH_BWD(GG) launch_bwd<OP, D, GG>(c, qt, kt, dot, lse, dbar, ucheck, dq32, dk32, dv32, dq0x, dk0x, ldt)
+#define SA_LAUNCH_BWD(GG) launch_bwd<OP, D, GG>(c, qt, kt, dot, lse, dbar, ucheck, dq0h, dk0h, dq0x, dk0x, ldt)
   if constexpr (sizeof(elem) == 2 && D <= 32) {
     if (G == 2) SA_LAUNCH_BWD(2);
     else SA_LAUNCH_BWD(1);
@@ -2323,16 +2341,14 @@ int backward_impl(const BwdCall& c) {
     SA_LAUNCH_BWD(1);
   }
 #undef SA_LAUNCH_BWD
-  const int64_t total = R * T * D;
-  const dim3 fgrid((unsigned)std::min<int64_t>(cdiv(total, NTHREADS), 8192));
-  if (c.grad_dtype == SA_DTYPE_F32)
-    hipLaunchKernelGGL((bwd_finish_kernel<float>), fgrid, dim3(NTHREADS), 0, st, dq32, dk32, dv32, dq0x, dk0x,
-                       static_cast<float*>(c.dq), static_cast<float*>(c.dk), static_cast<float*>(c.dv), c.dqs, c.dks,
-                       c.dvs, H, D, (int64_t)T * D, total, c.scale);
-  else
-    hipLaunchKernelGGL((bwd_finish_kernel<uint16_t>), fgrid, dim3(NTHREADS), 0, st, dq32, dk32, dv32, dq0x, dk0x,
-                       static_cast<uint16_t*>(c.dq), static_cast<uint16_t*>(c.dk), static_cast<uint16_t*>(c.dv),
-                       c.dqs, c.dks, c.dvs, H, D, (int64_t)T * D, total, c.scale);
+  // head 0's dQ, dK: its own sums plus the other groups' shares
+  const int64_t total4 = (int64_t)nseq * T * D / 4;
+  const int f32 = c.grad_dtype == SA_DTYPE_F32;
+  hipLaunchKernelGGL(bwd_finish_kernel, dim3((unsigned)std::min<int64_t>(cdiv(total4, NTHREADS), 8192)),
+                     dim3(NTHREADS), 0, st, reinterpret_cast<const float4*>(dq0h),
+                     reinterpret_cast<const float4*>(dk0h), reinterpret_cast<const float4*>(dq0x),
+                     reinterpret_cast<const float4*>(dk0x), GradView{c.dq, c.dqs, f32}, GradView{c.dk, c.dks, f32}, D,
+                     (int64_t)T * D, total4, c.scale);
   return launch_status();
 }
 
