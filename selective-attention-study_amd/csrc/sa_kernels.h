@@ -496,7 +496,11 @@ __device__ __forceinline__ float excl_scan32(float x) {
 
 // ---------------------------------------------------------------------------------------------
 // Selection column sums: colsum[b][rb][j] = sum over the queries r of block rb (chunk-relative)
-// of S[r, j]. One wavefront per key block; RB query blocks per workgroup row.
+// of S[r, j]. One wavefront per key block (its K rows in registers); a workgroup walks RB query
+// blocks, each staged once in LDS for its four wavefronts while the next one loads.
+#ifndef SA_SEL_RB
+#define SA_SEL_RB 8
+#endif
 
 template <class OP, int D>
 __global__ __launch_bounds__(NTHREADS) void sel_colsum_kernel(
@@ -506,40 +510,60 @@ __global__ __launch_bounds__(NTHREADS) void sel_colsum_kernel(
   using elem = typename OP::elem;
   using frag = typename OP::frag;
   constexpr int NS = D / OP::KS;
-  const int lane = threadIdx.x & 63, wave = wave_id();
+  constexpr int LDK = D + OP::KPAD;
+  __shared__ __attribute__((aligned(16))) elem sQ[2][TILE * LDK];   // query blocks, double-buffered
+  const int tid = threadIdx.x, lane = tid & 63, wave = wave_id();
   const int n = lane & 31, h = lane >> 5;
   const int NKT = (Tk + TILE - 1) / TILE;
   const int NBq = (Tq + TILE - 1) / TILE;
-  const int kb = blockIdx.x * NWAVES + wave;
-  if (kb >= NKT) return;
+  const int kb = blockIdx.x * NWAVES + wave;   // (a wavefront past the last key block only stages)
   const int b = blockIdx.z;
   const elem* q0 = q + qs.at(b, 0);
   const elem* k0 = k + ks.at(b, 0);
   const int j = kb * TILE + n;
+  const int kbase = kb * TILE;
 
   frag kf[NS];
 #pragma unroll
-  for (int s = 0; s < NS; ++s) kf[s] = ld_std_bounded<OP>(k0, ks.row, kb * TILE + n, Tk, h, s);
-
-  const int rb_end = min(NBq, (int)(blockIdx.y + 1) * RB);
-  for (int rb = blockIdx.y * RB; rb < rb_end; ++rb) {
+  for (int s = 0; s < NS; ++s) kf[s] = ld_std_bounded<OP>(k0, ks.row, kbase + n, Tk, h, s);
+  // a tile is interior when every pair passes: keys before every query, not exempt, queries
+  // before the end (keys past the end hold zero rows, their sums are never written)
+  const int rb0 = blockIdx.y * RB, rb_end = min(NBq, rb0 + RB);
+  RowTile<elem, D> nQ;
+  if (rb0 < rb_end) {
+    nQ.load(q0, qs.row, rb0 * TILE, Tq, tid);
+    nQ.template store<LDK>(sQ[0], tid);
+  }
+  __syncthreads();
+  for (int rb = rb0; rb < rb_end; ++rb) {
+    const int buf = (rb - rb0) & 1;
+    if (rb + 1 < rb_end) nQ.load(q0, qs.row, (rb + 1) * TILE, Tq, tid);   // the next block, into registers
     float cs = 0.f;
+    const int qbase = q_off + rb * TILE;   // absolute position of the block's first query
     // the tile holds a selectable pair only if some query is after the first key
-    if (q_off + rb * TILE + TILE - 1 > kb * TILE) {
+    if (kb < NKT && qbase + TILE - 1 > kbase) {
       f32x16 acc = zero16();
 #pragma unroll
-      for (int s = 0; s < NS; ++s)
-        acc = OP::mma(ld_std_bounded<OP>(q0, qs.row, rb * TILE + n, Tq, h, s), kf[s], acc);
+      for (int s = 0; s < NS; ++s) acc = OP::mma(OP::ld_std(sQ[buf], LDK, n, h, s), kf[s], acc);
+      // relu in unscaled logit units (relu(s x) = s relu(x), s > 0); the scale enters once
+      const bool interior = qbase > kbase + TILE - 1 && kbase >= exempt && rb * TILE + TILE <= Tq;
+      if (interior) {
 #pragma unroll
-      for (int i = 0; i < 16; ++i) {
-        const int r = rb * TILE + crow(i, h);
-        const float sv = acc[i] * scale;
-        const bool gate = (r < Tq) && (j >= exempt) && (j < q_off + r) && (sv > 0.f);
-        cs += gate ? sv : 0.f;
+        for (int i = 0; i < 16; ++i) cs += __builtin_amdgcn_fmed3f(acc[i], 0.f, 3.0e38f);
+      } else {
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+          const int r = rb * TILE + crow(i, h);
+          const bool gate = (r < Tq) && (j >= exempt) && (j < q_off + r) && (acc[i] > 0.f);
+          cs += gate ? acc[i] : 0.f;
+        }
       }
       cs += xor32(cs);
+      cs *= scale;
     }
-    if (h == 0 && j < Tk) colsum[((int64_t)b * NBq + rb) * Tk + j] = cs;
+    if (kb < NKT && h == 0 && j < Tk) colsum[((int64_t)b * NBq + rb) * Tk + j] = cs;
+    if (rb + 1 < rb_end) nQ.template store<LDK>(sQ[buf ^ 1], tid);
+    __syncthreads();
   }
 }
 
@@ -2189,7 +2213,7 @@ template <class OP, int D>
 int run_selection(const FwdCall& c, hipStream_t st) {
   using elem = typename OP::elem;
   const int NBq = (int)cdiv(c.Tq, TILE), NKT = (int)cdiv(c.Tk, TILE);
-  const int RB = 8;
+  const int RB = SA_SEL_RB;
   dim3 g1((unsigned)cdiv(NKT, NWAVES), (unsigned)cdiv(NBq, RB), (unsigned)c.nseq);
   TimedLaunch timed(SA_KERNEL_SELECTION, st);
   hipLaunchKernelGGL((sel_colsum_kernel<OP, D>), g1, dim3(NTHREADS), 0, st, static_cast<const elem*>(c.q),
