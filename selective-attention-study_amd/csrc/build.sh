@@ -5,9 +5,11 @@
 # Translation units, compiled in parallel:
 #   sa_bf16.hip  bf16-storage kernels, -amdgpu-mfma-vgpr-form: MFMA accumulators in VGPRs (left to
 #                its heuristics the compiler keeps them in AGPRs and copies every loop-carried
-#                accumulator back and forth each iteration)
-#   sa_bf16_kv.hip  the bf16 key-side backward kernel, the same flags plus the iterative ILP
-#                scheduler (faster for this kernel, slower for the others)
+#                accumulator back and forth each iteration), and the compiler's iterative ILP
+#                scheduler (faster for the tile loops than the default one)
+#   sa_bf16_kv.hip  the bf16 key-side backward kernel, the same flags, in a unit of its own (its
+#                template instances compile in parallel with the rest)
+#   sa_bf16_dec.hip  the bf16 decode-step kernels, the default scheduler (faster for them)
 #   sa_f32.hip   fp32-storage kernels, the compiler's own accumulator placement
 #   sa_abi.hip   the C ABI (host code only)
 # Every HIP compile: -packed-fp32-ops off (no v_pk_*_f32 from the compiler).
@@ -21,11 +23,14 @@ trap 'rm -rf "$tmp"' EXIT
 common=(--offload-arch=gfx950 -O3 -std=c++17 -fPIC -munsafe-fp-atomics
         -Xclang -target-feature -Xclang -packed-fp32-ops -I"$root/include" "$@")
 
-hipcc "${common[@]}" -mllvm -amdgpu-mfma-vgpr-form -c "$here/sa_bf16.hip" -o "$tmp/sa_bf16.o" &
+hipcc "${common[@]}" -mllvm -amdgpu-mfma-vgpr-form -mllvm -amdgpu-sched-strategy=iterative-ilp \
+  -c "$here/sa_bf16.hip" -o "$tmp/sa_bf16.o" &
 p1=$!
 hipcc "${common[@]}" -mllvm -amdgpu-mfma-vgpr-form -mllvm -amdgpu-sched-strategy=iterative-ilp \
   -c "$here/sa_bf16_kv.hip" -o "$tmp/sa_bf16_kv.o" &
 p4=$!
+hipcc "${common[@]}" -mllvm -amdgpu-mfma-vgpr-form -c "$here/sa_bf16_dec.hip" -o "$tmp/sa_bf16_dec.o" &
+p5=$!
 hipcc "${common[@]}" -c "$here/sa_f32.hip" -o "$tmp/sa_f32.o" &
 p2=$!
 hipcc "${common[@]}" -c "$here/sa_abi.hip" -o "$tmp/sa_abi.o" &
@@ -35,8 +40,10 @@ wait $p1 || rc=1
 wait $p2 || rc=1
 wait $p3 || rc=1
 wait $p4 || rc=1
+wait $p5 || rc=1
 [ $rc -eq 0 ] || { echo "build.sh: a compile failed" >&2; exit 1; }
-hipcc --offload-arch=gfx950 -shared -fPIC "$tmp/sa_bf16.o" "$tmp/sa_bf16_kv.o" "$tmp/sa_f32.o" "$tmp/sa_abi.o" \
+hipcc --offload-arch=gfx950 -shared -fPIC "$tmp/sa_bf16.o" "$tmp/sa_bf16_kv.o" "$tmp/sa_bf16_dec.o" "$tmp/sa_f32.o" \
+  "$tmp/sa_abi.o" \
   -o "$out.tmp"
 mv "$out.tmp" "$out"
 echo "built $out"

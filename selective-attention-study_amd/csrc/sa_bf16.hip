@@ -8,6 +8,5 @@ namespace sa_host {
 
 int forward_bf16(const FwdCall& c) { return forward_entry<OpBF16>(c); }
 int backward_bf16(const BwdCall& c) { return backward_entry<OpBF16>(c); }
-int decode_bf16(const DecCall& c) { return decode_entry<OpBF16>(c); }
 
 }  // namespace sa_host

@@ -1,6 +1,5 @@
-// The key-side backward kernel's bf16-storage instances, in a translation unit of their own:
-// build.sh compiles it with the compiler's iterative ILP scheduler (and the MFMA accumulators in
-// VGPRs, as sa_bf16.hip), which measures faster for this kernel and slower for the others.
+// The key-side backward kernel's bf16-storage instances, in a translation unit of their own (built
+// with the flags of sa_bf16.hip, in parallel with it).
 
 #include "sa_kernels.h"
 

@@ -231,7 +231,7 @@ SA_HIDDEN int forward_bf16(const FwdCall& c);    // sa_bf16.hip
 SA_HIDDEN int backward_bf16(const BwdCall& c);
 SA_HIDDEN int forward_f32(const FwdCall& c);     // sa_f32.hip
 SA_HIDDEN int backward_f32(const BwdCall& c);
-SA_HIDDEN int decode_bf16(const DecCall& c);
-SA_HIDDEN int decode_f32(const DecCall& c);
+SA_HIDDEN int decode_bf16(const DecCall& c);     // sa_bf16_dec.hip
+SA_HIDDEN int decode_f32(const DecCall& c);      // sa_f32.hip
 
 }  // namespace sa_host

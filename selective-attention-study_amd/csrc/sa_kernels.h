@@ -1765,9 +1765,10 @@ __global__ __launch_bounds__(NTHREADS, (dq_min_blocks<OP, D>())) void bwd_dq_ker
       __syncthreads();
     }
 
-    // (one loop for edge and interior tiles: split into an interior loop without the masks, the
-    // query side measured slower, unlike the forward and the key side)
-    for (int ktile = 0; ktile < wg_end; ++ktile) {
+    // one key tile; INTERIOR: no pair of the tile is masked or exempt for any wavefront, so the
+    // body is straight-line code without the masks
+    auto tile_step = [&](int ktile, auto interior_tag) {
+      constexpr bool INTERIOR = decltype(interior_tag)::value;
       const int kbase = ktile * TILE;
       const int buf = NBUF == 2 ? (ktile & 1) : 0;
       float hist, uin;
@@ -1788,7 +1789,7 @@ __global__ __launch_bounds__(NTHREADS, (dq_min_blocks<OP, D>())) void bwd_dq_ker
       if (ktile < my_end) {
         const int j = kbase + n;
         // tile body; edge: some pair of the tile is masked (diagonal, sequence end) or exempt
-        const bool edge = (kbase + TILE - 1 >= qbase) || (kbase + TILE > T) || kbase < exempt;
+        const bool edge = !INTERIOR && ((kbase + TILE - 1 >= qbase) || (kbase + TILE > T) || kbase < exempt);
         const TileMasks mk(j, qbase, T, exempt, h);
         {
           const elem* k0s = H0 ? sK[buf][0] : sK[buf][G];
@@ -1849,7 +1850,14 @@ __global__ __launch_bounds__(NTHREADS, (dq_min_blocks<OP, D>())) void bwd_dq_ker
         if (ktile + 1 < wg_end) store_tile(NBUF == 2 ? buf ^ 1 : 0);
         __syncthreads();
       }
-    }
+    };
+    // tiles holding exempt keys, then the interior ones (below every wavefront's diagonal, which
+    // also keeps them clear of the sequence end), then the diagonals
+    const int i_lo = min((exempt + TILE - 1) / TILE, wg_end);
+    const int i_hi = max(i_lo, min(qsb * NWAVES, wg_end));
+    for (int ktile = 0; ktile < i_lo; ++ktile) tile_step(ktile, std::false_type{});
+    for (int ktile = i_lo; ktile < i_hi; ++ktile) tile_step(ktile, std::true_type{});
+    for (int ktile = i_hi; ktile < wg_end; ++ktile) tile_step(ktile, std::false_type{});
   };
   if (has_h0) sweep(std::true_type{});
   else sweep(std::false_type{});
@@ -2292,8 +2300,7 @@ void launch_bwd(const BwdCall& c, const typename OP::elem* qt, const typename OP
     return s.row == D && s.head == (int64_t)c.T * D && s.seq == (int64_t)c.H * s.head;
   };
   const bool cv = contiguous(c.qs) && contiguous(c.ks) && contiguous(c.vs) && contiguous(c.dos);
-  // bf16: the key-side kernel lives in its own translation unit (sa_bf16_kv.hip), built with the
-  // compiler's iterative ILP scheduler, which measures faster for it (and slower for the others)
+  // bf16: the key-side kernel's instances live in a translation unit of their own (sa_bf16_kv.hip)
   const int f32 = c.grad_dtype == SA_DTYPE_F32;
   const GradView dqv{c.dq, c.dqs, f32}, dkv{c.dk, c.dks, f32}, dvv{c.dv, c.dvs, f32};
   const KvLaunch kv{q,    k,       v,      qt,   dout, dot,    c.qs, c.ks, c.vs, c.dos,    lse,      dbar,
