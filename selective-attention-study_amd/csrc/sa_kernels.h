@@ -88,11 +88,17 @@ __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_ex
 constexpr int RSRC_WORD3 = 0x00020000;
 
 // A 32 x 32 bf16 tile kept transposed in LDS for the transposing read ds_read_b64_tr_b16: rows of
-// 32 elements (64 bytes), the 8-byte chunk c of row r stored at chunk c ^ ((r / 4) mod 8). The
-// read gives lane i of each 16-lane group, element t, the element i % 4 of the 8 bytes that lane
-// 4t + i/4 of the group addresses (measured on gfx950). A lane-per-row write of one chunk from 32
-// rows, and a transposing read of four consecutive rows, then each touch every bank once.
-__device__ __forceinline__ int trt_off(int r, int c) { return r * 32 + ((c ^ ((r >> 2) & 7)) << 2); }
+// 32 elements (64 bytes), the 8-byte chunk c of row r stored at chunk c ^ sw(r / 2 mod 8), sw(a) =
+// 4 (a mod 2) + a / 2. The read gives lane i of each 16-lane group, element t, the element i % 4
+// of the 8 bytes that lane 4t + i/4 of the group addresses (measured on gfx950). The 8-byte
+// lane-per-row writes go to the banks 16 lanes at a time (32 banks of 4 bytes, as measured with the
+// bank-conflict counter): sixteen consecutive rows then hold one chunk in 16 distinct bank pairs
+// (rows of one parity take distinct chunks); a transposing read of four consecutive rows, chunks
+// 0-3 or 4-7, finds the two rows of each parity on opposite halves of the row.
+__device__ __forceinline__ int trt_off(int r, int c) {
+  const int a = (r >> 1) & 7;
+  return r * 32 + ((c ^ (((a & 1) << 2) | (a >> 1))) << 2);
+}
 
 typedef short short4v __attribute__((ext_vector_type(4)));
 
