@@ -1019,6 +1019,12 @@ __global__ __launch_bounds__(NTHREADS) void fill_zero_kernel(float4* __restrict_
 #ifndef SA_DQ_MIN_BLOCKS
 #define SA_DQ_MIN_BLOCKS 2
 #endif
+#ifndef SA_DQ_QLDS
+#define SA_DQ_QLDS 0   // 1: the query side's own Q, dO rows in LDS instead of registers
+#endif
+#ifndef SA_KV_K0REG
+#define SA_KV_K0REG 1   // the key side's copy of head 0's K rows in registers (0: in LDS)
+#endif
 // two workgroups per CU where their registers allow it (bf16, head dim <= 64)
 template <class OP, int D>
 constexpr int dq_min_blocks() { return (sizeof(typename OP::elem) == 2 && D <= 64) ? SA_DQ_MIN_BLOCKS : 1; }
@@ -1202,7 +1208,9 @@ __global__ __launch_bounds__(NTHREADS, (kv_min_blocks<OP, D, G>())) void bwd_kv_
   // Each wavefront's K and V rows (and head 0's K rows) are read from LDS per tile instead of being
   // held in registers, when they fit unpadded (swz64) beside the query tiles in half the CU's LDS:
   // the registers they free let two workgroups share a CU.
-  constexpr int NKV = 2 * G + 1;   // K, V of each head of the group, then head 0's K
+  // head 0's K rows of a group without head 0 in registers (SA_KV_K0REG) or in LDS
+  constexpr bool K0REG = SA_KV_K0REG != 0;
+  constexpr int NKV = 2 * G + (K0REG ? 0 : 1);   // K, V of each head of the group, then head 0's K
   constexpr int OTHER_LDS = NBUF * (TILE_BYTES + 2 * G * TILE * 4);
   constexpr bool KVLDS = sizeof(elem) == 2 && D == 64 && OTHER_LDS + NWAVES * NKV * TILE * D * 2 <= 80 * 1024;
   __shared__ __attribute__((aligned(16))) elem sKV[KVLDS ? NWAVES : 1][KVLDS ? NKV : 1][KVLDS ? TILE * D : 8];
@@ -1249,7 +1257,12 @@ __global__ __launch_bounds__(NTHREADS, (kv_min_blocks<OP, D, G>())) void bwd_kv_
         put(2 * g, view_head(k, ks, hd0 + g), view_ld(ks));
         put(2 * g + 1, view_head(v, vs, hd0 + g), view_ld(vs));
       }
-      if (!has_h0) put(2 * G, view_head(k, ks, 0), view_ld(ks));
+      if (!K0REG && !has_h0) put(2 * G, view_head(k, ks, 0), view_ld(ks));
+    }
+    if (K0REG && !has_h0) {
+      const elem* kh = view_head(k, ks, 0);
+#pragma unroll
+      for (int s = 0; s < NS; ++s) k0f[s] = ld_std_bounded<OP>(kh, view_ld(ks), j, T, h, s);
     }
   } else {
 #pragma unroll
@@ -1283,8 +1296,13 @@ __global__ __launch_bounds__(NTHREADS, (kv_min_blocks<OP, D, G>())) void bwd_kv_
   };
   // head 0's K: the group's own when it holds head 0 (h0)
   auto k0_frag = [&](bool h0, int s) -> frag {
-    if constexpr (KVLDS) return kv_lds(h0 ? 0 : 2 * G, s);
-    else return h0 ? kf[0][s] : k0f[s];
+    if constexpr (KVLDS) {
+      if (h0) return kv_lds(0, s);
+      if constexpr (K0REG) return k0f[s];
+      else return kv_lds(2 * G, s);
+    } else {
+      return h0 ? kf[0][s] : k0f[s];
+    }
   };
 
   f32x16 dkt[G][DB], dvt[G][DB], dk0t[DB];
@@ -1555,11 +1573,11 @@ __global__ __launch_bounds__(NTHREADS, (dq_min_blocks<OP, D>())) void bwd_dq_ker
   __shared__ __attribute__((aligned(16))) elem sZ[NWAVES][TILE * LDZ];
   __shared__ __attribute__((aligned(16))) float sLse[NWAVES][G][TILE];
   __shared__ __attribute__((aligned(16))) float sDb[NWAVES][G][TILE];
-  // Each wavefront's own Q and dO rows (A operands) are read from LDS per tile instead of being held
-  // in registers, when they fit beside the key tiles in half the CU's LDS: the registers they free
-  // let two workgroups share a CU.
+  // Each wavefront's own Q and dO rows (A operands) stay in registers (with SA_DQ_QLDS, in LDS when
+  // they fit beside the key tiles in half the CU's LDS: an option from when the registers they take
+  // would have cost the second workgroup per CU).
   constexpr int OTHER_LDS = NBUF * TILE_BYTES + NWAVES * (TILE * LDZ * (int)sizeof(elem) + 2 * G * TILE * 4);
-  constexpr bool QLDS = OTHER_LDS + 2 * NWAVES * G * TILE * LDK * (int)sizeof(elem) <= 80 * 1024;
+  constexpr bool QLDS = SA_DQ_QLDS && OTHER_LDS + 2 * NWAVES * G * TILE * LDK * (int)sizeof(elem) <= 80 * 1024;
   __shared__ __attribute__((aligned(16))) elem sQw[QLDS ? NWAVES : 1][G][QLDS ? TILE * LDK : 8];
   __shared__ __attribute__((aligned(16))) elem sdOw[QLDS ? NWAVES : 1][G][QLDS ? TILE * LDK : 8];
 
