@@ -1022,6 +1022,9 @@ __global__ __launch_bounds__(NTHREADS) void fill_zero_kernel(float4* __restrict_
 #ifndef SA_DQ_QLDS
 #define SA_DQ_QLDS 0   // 1: the query side's own Q, dO rows in LDS instead of registers
 #endif
+#ifndef SA_DQ_STATREG
+#define SA_DQ_STATREG 1   // the query side's row statistics (lse, dbar) in registers (0: in LDS)
+#endif
 #ifndef SA_KV_K0REG
 #define SA_KV_K0REG 1   // the key side's copy of head 0's K rows in registers (0: in LDS)
 #endif
@@ -1159,6 +1162,19 @@ __device__ __forceinline__ void p_dz_tile(const f32x16& lg, const f32x16& dpb, c
 #pragma unroll
     for (int i = 0; i < 16; ++i) dz[i] = pr[i] * dpb[i];
   }
+}
+
+// p_dz_tile with the rows' lse values already in registers (element i: row crow(i, h)).
+__device__ __forceinline__ void p_dz_tile_r(const f32x16& lg, const f32x16& dpb, const f32x16& lsev, float sl2,
+                                            bool edge, const TileMasks& mk, f32x16& pr, f32x16& dz) {
+#pragma unroll
+  for (int i = 0; i < 16; ++i) pr[i] = fast_exp2(fmaf(lg[i], sl2, -lsev[i]));
+  if (edge) {
+#pragma unroll
+    for (int i = 0; i < 16; ++i) pr[i] = crow(i, 0) >= mk.thr_p ? pr[i] : 0.f;
+  }
+#pragma unroll
+  for (int i = 0; i < 16; ++i) dz[i] = pr[i] * dpb[i];
 }
 
 // Whether some |g| of the wavefront's tile is large enough for the split-operand products: g sums
@@ -1571,8 +1587,10 @@ __global__ __launch_bounds__(NTHREADS, (dq_min_blocks<OP, D>())) void bwd_dq_ker
   __shared__ __attribute__((aligned(16))) elem sKt[NBUF][NH][D * LDKT];
   __shared__ __attribute__((aligned(16))) elem sV[NBUF][G][TILE * LDK];
   __shared__ __attribute__((aligned(16))) elem sZ[NWAVES][TILE * LDZ];
-  __shared__ __attribute__((aligned(16))) float sLse[NWAVES][G][TILE];
-  __shared__ __attribute__((aligned(16))) float sDb[NWAVES][G][TILE];
+  // the wavefront's row statistics: in registers (SA_DQ_STATREG) or in LDS rows
+  constexpr bool STATREG = SA_DQ_STATREG != 0;
+  __shared__ __attribute__((aligned(16))) float sLse[STATREG ? 1 : NWAVES][G][TILE];
+  __shared__ __attribute__((aligned(16))) float sDb[STATREG ? 1 : NWAVES][G][TILE];
   // Each wavefront's own Q and dO rows (A operands) stay in registers (with SA_DQ_QLDS, in LDS when
   // they fit beside the key tiles in half the CU's LDS: an option from when the registers they take
   // would have cost the second workgroup per CU).
@@ -1650,10 +1668,20 @@ __global__ __launch_bounds__(NTHREADS, (dq_min_blocks<OP, D>())) void bwd_dq_ker
     if constexpr (QLDS) return OP::ld_std(sdOw[wave][g], LDK, n, h, s);
     else return doa[g][s];
   };
+  f32x16 lse_r[STATREG ? G : 1], ndb_r[STATREG ? G : 1];
 #pragma unroll
   for (int g = 0; g < G; ++g) {
     const int64_t row = seq_row + hd0 + g;
-    if (lane < TILE) {
+    if constexpr (STATREG) {
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        const int r = qbase + crow(i, h);
+        const int rr = min(r, T - 1);
+        const float lv = lse[row * T + rr], dv_ = dbar[row * T + rr];
+        lse_r[g][i] = (r < T) ? lv : INFINITY;   // rows past the end: P = 0
+        ndb_r[g][i] = (r < T) ? -dv_ : 0.f;     // negated: dO.v accumulates onto it
+      }
+    } else if (lane < TILE) {
       const int r = qbase + lane;
       sLse[wave][g][lane] = (r < T) ? lse[row * T + r] : INFINITY;   // rows past the end: P = 0
       sDb[wave][g][lane] = (r < T) ? -dbar[row * T + r] : 0.f;   // negated: dO.v accumulates onto it
@@ -1838,12 +1866,15 @@ __global__ __launch_bounds__(NTHREADS, (dq_min_blocks<OP, D>())) void bwd_dq_ker
               for (int s = 0; s < NS; ++s)
                 lg = OP::mma(q_frag(g, s), OP::ld_std(sK[buf][g], LDK, n, h, s), lg);
             }
-            f32x16 dp = rows16(sDb[wave][g], h);   // dO.v - dbar
+            f32x16 dp;   // dO.v - dbar
+            if constexpr (STATREG) dp = ndb_r[g];
+            else dp = rows16(sDb[wave][g], h);
   #pragma unroll
             for (int s = 0; s < NS; ++s)
               dp = OP::mma(do_frag(g, s), OP::ld_std(sV[buf][g], LDK, n, h, s), dp);
             f32x16 pr, dz;
-            p_dz_tile<false>(lg, dp, sLse[wave][g], sl2, h, edge, mk, pr, dz);
+            if constexpr (STATREG) p_dz_tile_r(lg, dp, lse_r[g], sl2, edge, mk, pr, dz);
+            else p_dz_tile<false>(lg, dp, sLse[wave][g], sl2, h, edge, mk, pr, dz);
             if (g == 0) {
               zsum = dz;
             } else {
