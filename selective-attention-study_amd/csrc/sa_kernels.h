@@ -990,6 +990,55 @@ __global__ __launch_bounds__(NTHREADS) void transpose_kernel(const E* __restrict
   }
 }
 
+// The same transpose for 2-byte elements without LDS: a thread moves one 8 x 8 block (8 t, 8 d) --
+// eight 16-byte row loads (t past T read as zero), the block transposed in registers (each output
+// word joins the same half-word of two rows), eight 16-byte column stores. A wavefront's loads and
+// stores cover whole 128-byte segments (eight lanes per row or column).
+template <int D>
+__global__ __launch_bounds__(NTHREADS) void transpose8_kernel(const uint16_t* __restrict__ in,
+                                                              uint16_t* __restrict__ outT, int T, int64_t ldt,
+                                                              Strides is, int H) {
+  constexpr int CB = D / 8;   // 8-column blocks per row
+  const int64_t r = blockIdx.y;
+  const int c = threadIdx.x % CB;
+  const int64_t t0 = ((int64_t)blockIdx.x * (NTHREADS / CB) + threadIdx.x / CB) * 8;
+  if (t0 >= ldt) return;
+  const uint16_t* src = in + is.at(r / H, r % H) + 8 * c;
+  uint4 v[8];
+#pragma unroll
+  for (int k = 0; k < 8; ++k)
+    v[k] = (t0 + k < T) ? *reinterpret_cast<const uint4*>(src + (t0 + k) * is.row) : make_uint4(0u, 0u, 0u, 0u);
+  auto word = [&](int k, int w) -> uint32_t {
+    return w == 0 ? v[k].x : (w == 1 ? v[k].y : (w == 2 ? v[k].z : v[k].w));
+  };
+  uint16_t* dst = outT + r * D * ldt + t0;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    uint32_t o[4];
+#pragma unroll
+    for (int w = 0; w < 4; ++w) {
+      const uint32_t lo = word(2 * w, e >> 1), hi = word(2 * w + 1, e >> 1);
+      o[w] = (e & 1) ? ((lo >> 16) | (hi & 0xFFFF0000u)) : ((lo & 0xFFFFu) | (hi << 16));
+    }
+    *reinterpret_cast<uint4*>(dst + (int64_t)(8 * c + e) * ldt) = make_uint4(o[0], o[1], o[2], o[3]);
+  }
+}
+
+// in (R views, Strides is) -> outT (R, D, ldt), ldt a multiple of 64, zero past T.
+template <typename E, int D>
+void launch_transpose(const E* in, E* outT, int T, int64_t ldt, const Strides& is, int H, int64_t R,
+                      hipStream_t st) {
+  if constexpr (sizeof(E) == 2) {
+    constexpr int rows_per_block = NTHREADS / (D / 8) * 8;
+    hipLaunchKernelGGL((transpose8_kernel<D>), dim3((unsigned)cdiv(ldt, rows_per_block), (unsigned)R),
+                       dim3(NTHREADS), 0, st, reinterpret_cast<const uint16_t*>(in),
+                       reinterpret_cast<uint16_t*>(outT), T, ldt, is, H);
+  } else {
+    hipLaunchKernelGGL((transpose_kernel<E, D>), dim3((unsigned)cdiv(ldt, 64), (unsigned)R), dim3(NTHREADS), 0, st,
+                       in, outT, T, ldt, is, H);
+  }
+}
+
 __global__ __launch_bounds__(NTHREADS) void fill_zero_kernel(float4* __restrict__ p, int64_t n4) {
   for (int64_t i = (int64_t)blockIdx.x * NTHREADS + threadIdx.x; i < n4; i += (int64_t)gridDim.x * NTHREADS)
     p[i] = make_float4(0.f, 0.f, 0.f, 0.f);
@@ -1024,6 +1073,9 @@ __global__ __launch_bounds__(NTHREADS) void fill_zero_kernel(float4* __restrict_
 #endif
 #ifndef SA_DQ_STATREG
 #define SA_DQ_STATREG 1   // the query side's row statistics (lse, dbar) in registers (0: in LDS)
+#endif
+#ifndef SA_KV_KVLDS
+#define SA_KV_KVLDS 1   // the key side's own K, V rows in LDS (0: in registers)
 #endif
 #ifndef SA_KV_K0REG
 #define SA_KV_K0REG 1   // the key side's copy of head 0's K rows in registers (0: in LDS)
@@ -1228,7 +1280,7 @@ __global__ __launch_bounds__(NTHREADS, (kv_min_blocks<OP, D, G>())) void bwd_kv_
   constexpr bool K0REG = SA_KV_K0REG != 0;
   constexpr int NKV = 2 * G + (K0REG ? 0 : 1);   // K, V of each head of the group, then head 0's K
   constexpr int OTHER_LDS = NBUF * (TILE_BYTES + 2 * G * TILE * 4);
-  constexpr bool KVLDS = sizeof(elem) == 2 && D == 64 && OTHER_LDS + NWAVES * NKV * TILE * D * 2 <= 80 * 1024;
+  constexpr bool KVLDS = SA_KV_KVLDS && sizeof(elem) == 2 && D == 64 && OTHER_LDS + NWAVES * NKV * TILE * D * 2 <= 80 * 1024;
   __shared__ __attribute__((aligned(16))) elem sKV[KVLDS ? NWAVES : 1][KVLDS ? NKV : 1][KVLDS ? TILE * D : 8];
 
   const int tid = threadIdx.x, lane = tid & 63, wave = wave_id();
@@ -2311,9 +2363,7 @@ int forward_impl(const FwdCall& c) {
   using elem = typename OP::elem;
   const int64_t ldv = sa_transposed_ld(c.Tk);
   elem* vt = static_cast<elem*>(c.ws);
-  dim3 gt((unsigned)cdiv(ldv, 64), (unsigned)(c.nseq * c.H));
-  hipLaunchKernelGGL((transpose_kernel<elem, D>), gt, dim3(NTHREADS), 0, c.st, static_cast<const elem*>(c.v), vt,
-                     c.Tk, ldv, c.vs, c.H);
+  launch_transpose<elem, D>(static_cast<const elem*>(c.v), vt, c.Tk, ldv, c.vs, c.H, (int64_t)c.nseq * c.H, c.st);
   int rc = run_selection<OP, D>(c, c.st);
   if (rc) return rc;
   const int dtype = sizeof(elem) == 2 ? SA_DTYPE_BF16 : SA_DTYPE_F32;
@@ -2408,10 +2458,9 @@ int backward_impl(const BwdCall& c) {
   const elem* k = static_cast<const elem*>(c.k);
   const elem* dout = static_cast<const elem*>(c.dout);
 
-  dim3 gt((unsigned)cdiv(ldt, 64), (unsigned)R);
-  hipLaunchKernelGGL((transpose_kernel<elem, D>), gt, dim3(NTHREADS), 0, st, q, qt, T, ldt, c.qs, H);
-  hipLaunchKernelGGL((transpose_kernel<elem, D>), gt, dim3(NTHREADS), 0, st, dout, dot, T, ldt, c.dos, H);
-  hipLaunchKernelGGL((transpose_kernel<elem, D>), gt, dim3(NTHREADS), 0, st, k, kt, T, ldt, c.ks, H);
+  launch_transpose<elem, D>(q, qt, T, ldt, c.qs, H, R, st);
+  launch_transpose<elem, D>(dout, dot, T, ldt, c.dos, H, R, st);
+  launch_transpose<elem, D>(k, kt, T, ldt, c.ks, H, R, st);
   hipLaunchKernelGGL((bwd_rowstats_kernel<OP, D>), dim3((unsigned)cdiv(R * T * (D / 8), NTHREADS)), dim3(NTHREADS),
                      0, st, dout, c.dos, H, T, c.out, c.rmax, c.rden, lse, dbar, R * T);
   // head 0's shares from the other groups are atomic targets (one add per element and group)
