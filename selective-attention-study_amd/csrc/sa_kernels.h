@@ -756,8 +756,10 @@ __global__ __launch_bounds__(NTHREADS, (fwd_min_blocks<OP, D, G>())) void fwd_ke
 
   // one key tile; INTERIOR: every key of the tile strictly precedes every query of the workgroup,
   // lies before the end and is not exempt, for every wavefront (straight-line code without masks)
-  auto tile_step = [&](int t, auto interior_tag) {
+  // DAMP: history damping on (a compile-time fact, so the undamped loops carry no branch for it)
+  auto tile_step = [&](int t, auto interior_tag, auto damp_tag) __attribute__((always_inline)) {
     constexpr bool INTERIOR = decltype(interior_tag)::value;
+    constexpr bool DAMP = decltype(damp_tag)::value;
     const int kt = wg_end - 1 - t;
     const int buf = NBUF == 2 ? (t & 1) : 0;
     if (t + 1 < wg_end) load_tile(kt - 1);
@@ -819,7 +821,7 @@ __global__ __launch_bounds__(NTHREADS, (fwd_min_blocks<OP, D, G>())) void fwd_ke
           fs[4 * a + 2] = f4.z;
           fs[4 * a + 3] = f4.w;
         }
-        if (damp_mode != 0) {
+        if constexpr (DAMP) {
 #pragma unroll
           for (int i = 0; i < 16; ++i) fs[i] *= damp;
         }
@@ -877,10 +879,14 @@ __global__ __launch_bounds__(NTHREADS, (fwd_min_blocks<OP, D, G>())) void fwd_ke
   // [i_lo, i_hi), then the tiles holding exempt keys
   const int i_lo = min((exempt + TILE - 1) / TILE, wg_end);
   const int i_hi = max(i_lo, min(min(q_off + qsb * NWAVES * TILE, Tk) / TILE, wg_end));
-  int t = 0;
-  for (; t < wg_end - i_hi; ++t) tile_step(t, std::false_type{});
-  for (; t < wg_end - i_lo; ++t) tile_step(t, std::true_type{});
-  for (; t < wg_end; ++t) tile_step(t, std::false_type{});
+  auto sweep = [&](auto damp_tag) {
+    int t = 0;
+    for (; t < wg_end - i_hi; ++t) tile_step(t, std::false_type{}, damp_tag);
+    for (; t < wg_end - i_lo; ++t) tile_step(t, std::true_type{}, damp_tag);
+    for (; t < wg_end; ++t) tile_step(t, std::false_type{}, damp_tag);
+  };
+  if (damp_mode != 0) sweep(std::true_type{});
+  else sweep(std::false_type{});
 
   if (rb >= NBq || q_rel >= Tq) return;
 #pragma unroll
@@ -926,10 +932,16 @@ template <class OP, int D>
 __global__ __launch_bounds__(NTHREADS) void bwd_rowstats_kernel(
     const typename OP::elem* __restrict__ dout, Strides dos, int H, int T, const float* __restrict__ out,
     const float* __restrict__ rmax, const float* __restrict__ rden,
-    float* __restrict__ lse, float* __restrict__ dbar, int64_t rows) {
+    float* __restrict__ lse, float* __restrict__ dbar, int64_t rows, float4* __restrict__ zero0,
+    float4* __restrict__ zero1, int64_t zero_n4) {
   using elem = typename OP::elem;
   constexpr int LPR = D / 8;   // lanes per row
   const int64_t g = (int64_t)blockIdx.x * NTHREADS + threadIdx.x;
+  // also clears the targets of the head-0 share atomics (zero_n4 float4s each)
+  for (int64_t i = g; i < zero_n4; i += (int64_t)gridDim.x * NTHREADS) {
+    zero0[i] = make_float4(0.f, 0.f, 0.f, 0.f);
+    zero1[i] = make_float4(0.f, 0.f, 0.f, 0.f);
+  }
   const int64_t r = g / LPR;
   const int part = (int)(g % LPR);
   float acc = 0.f;
@@ -1037,11 +1049,6 @@ void launch_transpose(const E* in, E* outT, int T, int64_t ldt, const Strides& i
     hipLaunchKernelGGL((transpose_kernel<E, D>), dim3((unsigned)cdiv(ldt, 64), (unsigned)R), dim3(NTHREADS), 0, st,
                        in, outT, T, ldt, is, H);
   }
-}
-
-__global__ __launch_bounds__(NTHREADS) void fill_zero_kernel(float4* __restrict__ p, int64_t n4) {
-  for (int64_t i = (int64_t)blockIdx.x * NTHREADS + threadIdx.x; i < n4; i += (int64_t)gridDim.x * NTHREADS)
-    p[i] = make_float4(0.f, 0.f, 0.f, 0.f);
 }
 
 // ---------------------------------------------------------------------------------------------
@@ -2462,12 +2469,11 @@ int backward_impl(const BwdCall& c) {
   launch_transpose<elem, D>(dout, dot, T, ldt, c.dos, H, R, st);
   launch_transpose<elem, D>(k, kt, T, ldt, c.ks, H, R, st);
   hipLaunchKernelGGL((bwd_rowstats_kernel<OP, D>), dim3((unsigned)cdiv(R * T * (D / 8), NTHREADS)), dim3(NTHREADS),
-                     0, st, dout, c.dos, H, T, c.out, c.rmax, c.rden, lse, dbar, R * T);
-  // head 0's shares from the other groups are atomic targets (one add per element and group)
-  hipLaunchKernelGGL(fill_zero_kernel, dim3(256), dim3(NTHREADS), 0, st, reinterpret_cast<float4*>(dq0x),
-                     (int64_t)((int64_t)nseq * T * D / 4));
-  hipLaunchKernelGGL(fill_zero_kernel, dim3(256), dim3(NTHREADS), 0, st, reinterpret_cast<float4*>(dk0x),
-                     (int64_t)((int64_t)nseq * T * D / 4));
+                     0, st, dout, c.dos, H, T, c.out, c.rmax, c.rden, lse, dbar, R * T,
+                     // head 0's shares from the other groups are atomic targets (one add per element
+                     // and group): cleared here
+                     reinterpret_cast<float4*>(dq0x), reinterpret_cast<float4*>(dk0x),
+                     (int64_t)nseq * T * D / 4);
 #define SA_LAUNCH_BWD(GG) launch_bwd<OP, D, GG>(c, qt, kt, dot, lse, dbar, ucheck, dq0h, dk0h, dq0x, dk0x, ldt)
   if constexpr (sizeof(elem) == 2 && D <= 32) {
     if (G == 2) SA_LAUNCH_BWD(2);
