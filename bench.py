@@ -43,9 +43,9 @@ KERNEL_FLOP = {"forward": 2.0 * UNIT, "backward_kv": 4.0 * UNIT, "backward_dq": 
 # WRITE_SIZE counters (one pass each) and scaled by a 1 GiB copy's readings (FETCH x 2.0, WRITE x
 # 1.0): profiles/c2_attention_kernels_traffic.md. The counters need the profiler, so bench.py
 # reports the committed measurement; re-measure after a kernel change.
-MEASURED_TRAFFIC_BYTES = {"forward": (2.0 * 526_917 + 67_584) * 1024,
-                          "backward_kv": (2.0 * 591_075 + 576_555) * 1024,
-                          "backward_dq": (2.0 * 531_895 + 96_256) * 1024}
+MEASURED_TRAFFIC_BYTES = {"forward": (2.0 * 530_879 + 67_584) * 1024,
+                          "backward_kv": (2.0 * 582_772 + 576_429) * 1024,
+                          "backward_dq": (2.0 * 541_704 + 96_256) * 1024}
 
 
 def _cpu_model() -> str:
