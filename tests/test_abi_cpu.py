@@ -131,13 +131,16 @@ def test_strided_views_are_validated_before_any_launch():
     assert fwd(y=fake, ys=None) == -1                     # output without a view
     assert fwd(qs=V(16 * 768, 64, 1 << 27)) == -1         # rows past the 2 GiB a head may span
 
-    def bwd(dqs=good, dos=good):
+    def bwd(dqs=good, dos=good, dq=fake, dv=fake):
         return lib.sa_backward_strided(fake, good, fake, good, fake, good, fake, fake, dos, fake, fake, fake,
-                                       fake, dqs, fake, good, fake, good, fake, ws, 1, 4, 16, 64, 0.125, 0, 0, 1,
+                                       dq, dqs, fake, good, dv, good, fake, ws, 1, 4, 16, 64, 0.125, 0, 0, 1,
                                        0, None)
 
     assert bwd(dqs=V(0, 16, 768)) == -1                   # gradient heads overlap
     assert bwd(dos=V(0, 64, 60)) == -1                    # dout row stride below head_dim
+    # gradients are written in 8- and 16-byte pieces straight into the views
+    assert bwd(dq=fake + 8) == -1                         # gradient pointer not 16-byte aligned
+    assert bwd(dv=fake + 2) == -1
 
 
 def test_api_checks_on_cpu_tensors():
