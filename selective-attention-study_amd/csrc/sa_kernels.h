@@ -615,6 +615,9 @@ __global__ __launch_bounds__(NTHREADS) void sel_scan_kernel(
 #ifndef SA_FWD_NBUF
 #define SA_FWD_NBUF 2   // LDS buffers of the key tiles (2: the next tile is written while one is read)
 #endif
+#ifndef SA_FWD_PIPE
+#define SA_FWD_PIPE 1   // 1: the next key tile loads during this one (double-buffered LDS)
+#endif
 #ifndef SA_FWD_MIN_BLOCKS
 #define SA_FWD_MIN_BLOCKS 3
 #endif
@@ -640,7 +643,7 @@ __global__ __launch_bounds__(NTHREADS, (fwd_min_blocks<OP, D, G>())) void fwd_ke
   constexpr int AS = OP::acc_steps;
   constexpr int NH = G + 1;
   constexpr int TILE_BYTES = (NH * TILE * LDK + G * D * LDV) * (int)sizeof(elem);
-  constexpr int NBUF = (SA_FWD_NBUF >= 2 && 2 * TILE_BYTES <= 120 * 1024) ? 2 : 1;
+  constexpr int NBUF = (SA_FWD_PIPE && SA_FWD_NBUF >= 2 && 2 * TILE_BYTES <= 120 * 1024) ? 2 : 1;
 
   __shared__ __attribute__((aligned(16))) elem sK[NBUF][NH][TILE * LDK];
   __shared__ __attribute__((aligned(16))) elem sVt[NBUF][G][D * LDV];
@@ -750,9 +753,14 @@ __global__ __launch_bounds__(NTHREADS, (fwd_min_blocks<OP, D, G>())) void fwd_ke
     if (tid < NWAVES * TILE) sC[buf][tid >> 5][tid & (TILE - 1)] = nC;
   };
 
-  load_tile(wg_end - 1);
-  store_tile(0);
-  __syncthreads();
+  // FWD_PIPE: the next key tile is loaded into registers while this one is computed (stored to
+  // the other LDS buffer after it); else each tile is loaded and stored at its own step's start
+  constexpr bool FWD_PIPE = SA_FWD_PIPE != 0;
+  if constexpr (FWD_PIPE) {
+    load_tile(wg_end - 1);
+    store_tile(0);
+    __syncthreads();
+  }
 
   // one key tile; INTERIOR: every key of the tile strictly precedes every query of the workgroup,
   // lies before the end and is not exempt, for every wavefront (straight-line code without masks)
@@ -761,8 +769,15 @@ __global__ __launch_bounds__(NTHREADS, (fwd_min_blocks<OP, D, G>())) void fwd_ke
     constexpr bool INTERIOR = decltype(interior_tag)::value;
     constexpr bool DAMP = decltype(damp_tag)::value;
     const int kt = wg_end - 1 - t;
-    const int buf = NBUF == 2 ? (t & 1) : 0;
-    if (t + 1 < wg_end) load_tile(kt - 1);
+    const int buf = (FWD_PIPE && NBUF == 2) ? (t & 1) : 0;
+    if constexpr (FWD_PIPE) {
+      if (t + 1 < wg_end) load_tile(kt - 1);
+    } else {
+      load_tile(kt);
+      if (t > 0) __syncthreads();   // every wavefront is done with the previous tile
+      store_tile(0);
+      __syncthreads();
+    }
     if (kt < my_end) {   // (a wavefront past the last query block has none)
       const int kbase = kt * TILE;
       // edge: some key of the tile does not strictly precede every query of the block, lies past
@@ -871,9 +886,11 @@ __global__ __launch_bounds__(NTHREADS, (fwd_min_blocks<OP, D, G>())) void fwd_ke
       };
       body();
     }
-    if constexpr (NBUF == 1) __syncthreads();   // the one buffer is free again
-    if (t + 1 < wg_end) store_tile(NBUF == 2 ? buf ^ 1 : 0);
-    __syncthreads();
+    if constexpr (FWD_PIPE) {
+      if constexpr (NBUF == 1) __syncthreads();   // the one buffer is free again
+      if (t + 1 < wg_end) store_tile(NBUF == 2 ? buf ^ 1 : 0);
+      __syncthreads();
+    }
   };
   // key tiles newest first: the diagonals and the sequence end, the interior tiles
   // [i_lo, i_hi), then the tiles holding exempt keys
