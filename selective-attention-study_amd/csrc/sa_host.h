@@ -68,15 +68,12 @@ inline int launch_status() { return hipGetLastError() == hipSuccess ? SA_OK : SA
 // Heads per wavefront of the forward (a group shares head 0's selection work: its logits, F):
 // 4 at head dim <= 32, 2 at 64 (two heads' output sums in registers leave two workgroups per CU,
 // which measures faster than three with one head), 1 beyond; fp32 storage 1.
-#ifndef SA_FWD_GROUP_D64
-#define SA_FWD_GROUP_D64 2
-#endif
 inline int auto_group(int dtype, int64_t D, int64_t heads, int requested, bool backward) {
   int g = requested;
   if (g <= 0) {
     if (dtype == SA_DTYPE_F32) g = 1;
     else if (backward) g = (D <= 32) ? 2 : 1;
-    else g = (D <= 32) ? 4 : (D <= 64 ? SA_FWD_GROUP_D64 : 1);
+    else g = (D <= 32) ? 4 : (D <= 64 ? 2 : 1);
   }
   int cap = (dtype == SA_DTYPE_F32) ? 1 : (backward ? 2 : 4);
   if (D >= 128 || (backward && D >= 64)) cap = 1;
@@ -86,12 +83,10 @@ inline int auto_group(int dtype, int64_t D, int64_t heads, int requested, bool b
 }
 
 // Heads per wavefront of the backward kernels: a group shares head 0's selection work (its logits,
-// the history F and the g products), so wider groups amortise it, within the register budget.
-#ifndef SA_BWD_GROUP_DEFAULT
-#define SA_BWD_GROUP_DEFAULT 1
-#endif
+// the history F and the g products), so wider groups amortise it, within the register budget; by
+// default one head (two heads per wavefront cost the second workgroup per CU, measured slower).
 inline int bwd_group(int dtype, int64_t D, int64_t heads, int requested) {
-  int g = requested > 0 ? requested : SA_BWD_GROUP_DEFAULT;
+  int g = requested > 0 ? requested : 1;
   const int cap = (dtype == SA_DTYPE_BF16 && D <= 32) ? 2 : 1;
   g = g > cap ? cap : g;
   while (g > 1 && (heads % g != 0)) g >>= 1;

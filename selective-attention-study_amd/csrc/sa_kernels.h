@@ -331,9 +331,6 @@ __device__ __forceinline__ void stage_cols(E* s, const E* g, int64_t gld, int co
 // kernels remap the linear workgroup id so that every XCD takes a contiguous range of the
 // (head group, block) order instead: the workgroups one L2 serves at a time then belong to one or
 // two heads and share that head's tiles.
-#ifndef SA_XCD_REMAP
-#define SA_XCD_REMAP 1
-#endif
 constexpr int NXCD = 8;
 struct BlockXY {
   int x, y;
@@ -342,7 +339,7 @@ __device__ __forceinline__ BlockXY xcd_block() {
   const int gx = gridDim.x, n = gx * gridDim.y;
   const int l = blockIdx.x + gx * blockIdx.y;
   const int per = n / NXCD;
-  const int m = (SA_XCD_REMAP && l < per * NXCD) ? (l % NXCD) * per + l / NXCD : l;
+  const int m = (l < per * NXCD) ? (l % NXCD) * per + l / NXCD : l;
   return {m % gx, m / gx};
 }
 
@@ -504,9 +501,7 @@ __device__ __forceinline__ float excl_scan32(float x) {
 // Selection column sums: colsum[b][rb][j] = sum over the queries r of block rb (chunk-relative)
 // of S[r, j]. One wavefront per key block (its K rows in registers); a workgroup walks RB query
 // blocks, each staged once in LDS for its four wavefronts while the next one loads.
-#ifndef SA_SEL_RB
-#define SA_SEL_RB 8
-#endif
+constexpr int SEL_RB = 8;   // query blocks per workgroup
 
 template <class OP, int D>
 __global__ __launch_bounds__(NTHREADS) void sel_colsum_kernel(
@@ -611,18 +606,9 @@ __global__ __launch_bounds__(NTHREADS) void sel_scan_kernel(
 // tile's K, V^T and carry rows are loaded while the current one is computed (double-buffered LDS).
 
 // Workgroups per CU the forward's register allocation must allow: three at bf16 head dims <= 64
-// (its LDS fits three), which holds it to 168 registers without spills.
-#ifndef SA_FWD_NBUF
-#define SA_FWD_NBUF 2   // LDS buffers of the key tiles (2: the next tile is written while one is read)
-#endif
-#ifndef SA_FWD_PIPE
-#define SA_FWD_PIPE 1   // 1: the next key tile loads during this one (double-buffered LDS)
-#endif
-#ifndef SA_FWD_MIN_BLOCKS
-#define SA_FWD_MIN_BLOCKS 3
-#endif
+// with one head per wavefront (its LDS fits three), which holds it to 168 registers without spills.
 template <class OP, int D, int G>
-constexpr int fwd_min_blocks() { return (sizeof(typename OP::elem) == 2 && D <= 64 && G == 1) ? SA_FWD_MIN_BLOCKS : 1; }
+constexpr int fwd_min_blocks() { return (sizeof(typename OP::elem) == 2 && D <= 64 && G == 1) ? 3 : 1; }
 
 // CV ("contiguous views"): q rows are D apart and its heads Tq * D apart, k rows D apart and its
 // heads ks.head apart -- the layout of sa_forward; the view strides are then compile-time facts
@@ -643,7 +629,8 @@ __global__ __launch_bounds__(NTHREADS, (fwd_min_blocks<OP, D, G>())) void fwd_ke
   constexpr int AS = OP::acc_steps;
   constexpr int NH = G + 1;
   constexpr int TILE_BYTES = (NH * TILE * LDK + G * D * LDV) * (int)sizeof(elem);
-  constexpr int NBUF = (SA_FWD_PIPE && SA_FWD_NBUF >= 2 && 2 * TILE_BYTES <= 120 * 1024) ? 2 : 1;
+  // two LDS buffers of the key tiles (the next one is written while this one is read) when they fit
+  constexpr int NBUF = (2 * TILE_BYTES <= 120 * 1024) ? 2 : 1;
 
   __shared__ __attribute__((aligned(16))) elem sK[NBUF][NH][TILE * LDK];
   __shared__ __attribute__((aligned(16))) elem sVt[NBUF][G][D * LDV];
@@ -753,14 +740,11 @@ __global__ __launch_bounds__(NTHREADS, (fwd_min_blocks<OP, D, G>())) void fwd_ke
     if (tid < NWAVES * TILE) sC[buf][tid >> 5][tid & (TILE - 1)] = nC;
   };
 
-  // FWD_PIPE: the next key tile is loaded into registers while this one is computed (stored to
-  // the other LDS buffer after it); else each tile is loaded and stored at its own step's start
-  constexpr bool FWD_PIPE = SA_FWD_PIPE != 0;
-  if constexpr (FWD_PIPE) {
-    load_tile(wg_end - 1);
-    store_tile(0);
-    __syncthreads();
-  }
+  // the next key tile is loaded into registers while this one is computed (stored to the other LDS
+  // buffer after it)
+  load_tile(wg_end - 1);
+  store_tile(0);
+  __syncthreads();
 
   // one key tile; INTERIOR: every key of the tile strictly precedes every query of the workgroup,
   // lies before the end and is not exempt, for every wavefront (straight-line code without masks)
@@ -769,15 +753,8 @@ __global__ __launch_bounds__(NTHREADS, (fwd_min_blocks<OP, D, G>())) void fwd_ke
     constexpr bool INTERIOR = decltype(interior_tag)::value;
     constexpr bool DAMP = decltype(damp_tag)::value;
     const int kt = wg_end - 1 - t;
-    const int buf = (FWD_PIPE && NBUF == 2) ? (t & 1) : 0;
-    if constexpr (FWD_PIPE) {
-      if (t + 1 < wg_end) load_tile(kt - 1);
-    } else {
-      load_tile(kt);
-      if (t > 0) __syncthreads();   // every wavefront is done with the previous tile
-      store_tile(0);
-      __syncthreads();
-    }
+    const int buf = NBUF == 2 ? (t & 1) : 0;
+    if (t + 1 < wg_end) load_tile(kt - 1);
     if (kt < my_end) {   // (a wavefront past the last query block has none)
       const int kbase = kt * TILE;
       // edge: some key of the tile does not strictly precede every query of the block, lies past
@@ -886,11 +863,9 @@ __global__ __launch_bounds__(NTHREADS, (fwd_min_blocks<OP, D, G>())) void fwd_ke
       };
       body();
     }
-    if constexpr (FWD_PIPE) {
-      if constexpr (NBUF == 1) __syncthreads();   // the one buffer is free again
-      if (t + 1 < wg_end) store_tile(NBUF == 2 ? buf ^ 1 : 0);
-      __syncthreads();
-    }
+    if constexpr (NBUF == 1) __syncthreads();   // the one buffer is free again
+    if (t + 1 < wg_end) store_tile(NBUF == 2 ? buf ^ 1 : 0);
+    __syncthreads();
   };
   // key tiles newest first: the diagonals and the sequence end, the interior tiles
   // [i_lo, i_hi), then the tiles holding exempt keys
@@ -1069,46 +1044,14 @@ void launch_transpose(const E* in, E* outT, int T, int64_t ldt, const Strides& i
 }
 
 // ---------------------------------------------------------------------------------------------
-// Backward kernel shapes. *_PIPE 1: the next tile's global loads are issued before the current tile
-// is computed (double-buffered LDS when it fits); 0: load, store, compute in turn, leaving the
-// overlap to another workgroup on the CU. *_MIN_BLOCKS: workgroups per CU the register
-// allocation must allow.
-// Both sides fit two workgroups per CU at bf16 head dims <= 64 once their per-wavefront operands
-// (the key side's K and V rows, the query side's Q and dO rows) sit in LDS instead of registers;
-// the second workgroup then hides LDS and memory latency better than pipelining the loads.
-#ifndef SA_KV_PIPE
-#define SA_KV_PIPE 0
-#endif
-#ifndef SA_KV_MIN_BLOCKS
-#define SA_KV_MIN_BLOCKS 2
-#endif
-
-#ifndef SA_DQ_PIPE
-#define SA_DQ_PIPE 0
-#endif
-#ifndef SA_DQ_NBUF
-#define SA_DQ_NBUF 2
-#endif
-#ifndef SA_DQ_MIN_BLOCKS
-#define SA_DQ_MIN_BLOCKS 2
-#endif
-#ifndef SA_DQ_QLDS
-#define SA_DQ_QLDS 0   // 1: the query side's own Q, dO rows in LDS instead of registers
-#endif
-#ifndef SA_DQ_STATREG
-#define SA_DQ_STATREG 1   // the query side's row statistics (lse, dbar) in registers (0: in LDS)
-#endif
-#ifndef SA_KV_KVLDS
-#define SA_KV_KVLDS 1   // the key side's own K, V rows in LDS (0: in registers)
-#endif
-#ifndef SA_KV_K0REG
-#define SA_KV_K0REG 1   // the key side's copy of head 0's K rows in registers (0: in LDS)
-#endif
-// two workgroups per CU where their registers allow it (bf16, head dim <= 64)
+// Backward kernel shapes. Each tile is loaded, stored to LDS and computed in turn (one LDS buffer):
+// a second workgroup on the CU hides the load latency better than pipelining the loads would
+// (measured). Both sides fit two workgroups per CU at bf16 head dims <= 64: the key side's K and V
+// rows sit in LDS, the query side's Q and dO rows and row statistics in registers.
 template <class OP, int D>
-constexpr int dq_min_blocks() { return (sizeof(typename OP::elem) == 2 && D <= 64) ? SA_DQ_MIN_BLOCKS : 1; }
+constexpr int dq_min_blocks() { return (sizeof(typename OP::elem) == 2 && D <= 64) ? 2 : 1; }
 template <class OP, int D, int G>
-constexpr int kv_min_blocks() { return (sizeof(typename OP::elem) == 2 && D <= 64 && G == 1) ? SA_KV_MIN_BLOCKS : 1; }
+constexpr int kv_min_blocks() { return (sizeof(typename OP::elem) == 2 && D <= 64 && G == 1) ? 2 : 1; }
 
 // ---------------------------------------------------------------------------------------------
 // Gradient stores to a caller's view (fp32 or bf16 elements): one element, or four consecutive
@@ -1286,25 +1229,21 @@ __global__ __launch_bounds__(NTHREADS, (kv_min_blocks<OP, D, G>())) void bwd_kv_
   constexpr int LDV = TILE + OP::TPAD;
   constexpr int AS = OP::acc_steps;
   constexpr int NH = G + 1;   // staged heads: the group, then head 0 when outside the group
-  constexpr bool KV_PIPE = SA_KV_PIPE != 0;
-  // two buffers (the tile being computed, the next one being written) when they fit in LDS
   constexpr int TILE_BYTES = (NH * (TILE * LDK + D * LDV) + G * (TILE * LDK + D * LDV)) * (int)sizeof(elem);
-  constexpr int NBUF = (KV_PIPE && 2 * TILE_BYTES <= 120 * 1024) ? 2 : 1;
 
-  __shared__ __attribute__((aligned(16))) elem sQ[NBUF][NH][TILE * LDK];
-  __shared__ __attribute__((aligned(16))) elem sQt[NBUF][NH][D * LDV];
-  __shared__ __attribute__((aligned(16))) elem sdO[NBUF][G][TILE * LDK];
-  __shared__ __attribute__((aligned(16))) elem sdOt[NBUF][G][D * LDV];
-  __shared__ __attribute__((aligned(16))) float sLse[NBUF][G][TILE];
-  __shared__ __attribute__((aligned(16))) float sDb[NBUF][G][TILE];
-  // Each wavefront's K and V rows (and head 0's K rows) are read from LDS per tile instead of being
-  // held in registers, when they fit unpadded (swz64) beside the query tiles in half the CU's LDS:
-  // the registers they free let two workgroups share a CU.
-  // head 0's K rows of a group without head 0 in registers (SA_KV_K0REG) or in LDS
-  constexpr bool K0REG = SA_KV_K0REG != 0;
-  constexpr int NKV = 2 * G + (K0REG ? 0 : 1);   // K, V of each head of the group, then head 0's K
-  constexpr int OTHER_LDS = NBUF * (TILE_BYTES + 2 * G * TILE * 4);
-  constexpr bool KVLDS = SA_KV_KVLDS && sizeof(elem) == 2 && D == 64 && OTHER_LDS + NWAVES * NKV * TILE * D * 2 <= 80 * 1024;
+  __shared__ __attribute__((aligned(16))) elem sQ[NH][TILE * LDK];
+  __shared__ __attribute__((aligned(16))) elem sQt[NH][D * LDV];
+  __shared__ __attribute__((aligned(16))) elem sdO[G][TILE * LDK];
+  __shared__ __attribute__((aligned(16))) elem sdOt[G][D * LDV];
+  __shared__ __attribute__((aligned(16))) float sLse[G][TILE];
+  __shared__ __attribute__((aligned(16))) float sDb[G][TILE];
+  // Each wavefront's K and V rows are read from LDS per tile instead of being held in registers,
+  // when they fit unpadded (swz64) beside the query tiles in half the CU's LDS: the registers they
+  // free let two workgroups share a CU. Head 0's K rows (for a group without head 0) stay in
+  // registers.
+  constexpr int NKV = 2 * G;   // K, V of each head of the group
+  constexpr int OTHER_LDS = TILE_BYTES + 2 * G * TILE * 4;
+  constexpr bool KVLDS = sizeof(elem) == 2 && D == 64 && OTHER_LDS + NWAVES * NKV * TILE * D * 2 <= 80 * 1024;
   __shared__ __attribute__((aligned(16))) elem sKV[KVLDS ? NWAVES : 1][KVLDS ? NKV : 1][KVLDS ? TILE * D : 8];
 
   const int tid = threadIdx.x, lane = tid & 63, wave = wave_id();
@@ -1349,9 +1288,8 @@ __global__ __launch_bounds__(NTHREADS, (kv_min_blocks<OP, D, G>())) void bwd_kv_
         put(2 * g, view_head(k, ks, hd0 + g), view_ld(ks));
         put(2 * g + 1, view_head(v, vs, hd0 + g), view_ld(vs));
       }
-      if (!K0REG && !has_h0) put(2 * G, view_head(k, ks, 0), view_ld(ks));
     }
-    if (K0REG && !has_h0) {
+    if (!has_h0) {
       const elem* kh = view_head(k, ks, 0);
 #pragma unroll
       for (int s = 0; s < NS; ++s) k0f[s] = ld_std_bounded<OP>(kh, view_ld(ks), j, T, h, s);
@@ -1389,9 +1327,7 @@ __global__ __launch_bounds__(NTHREADS, (kv_min_blocks<OP, D, G>())) void bwd_kv_
   // head 0's K: the group's own when it holds head 0 (h0)
   auto k0_frag = [&](bool h0, int s) -> frag {
     if constexpr (KVLDS) {
-      if (h0) return kv_lds(0, s);
-      if constexpr (K0REG) return k0f[s];
-      else return kv_lds(2 * G, s);
+      return h0 ? kv_lds(0, s) : k0f[s];
     } else {
       return h0 ? kf[0][s] : k0f[s];
     }
@@ -1449,21 +1385,21 @@ __global__ __launch_bounds__(NTHREADS, (kv_min_blocks<OP, D, G>())) void bwd_kv_
       nQt[G].load(qt + seq_row * D * ldt, ldt, qbase, tid);
     }
   };
-  auto store_tile = [&](int buf) {
+  auto store_tile = [&]() {
 #pragma unroll
     for (int g = 0; g < G; ++g) {
-      nQ[g].template store<LDK>(sQ[buf][g], tid);
-      nQt[g].template store_crow<LDV>(sQt[buf][g], tid);
-      ndO[g].template store<LDK>(sdO[buf][g], tid);
-      ndOt[g].template store_crow<LDV>(sdOt[buf][g], tid);
+      nQ[g].template store<LDK>(sQ[g], tid);
+      nQt[g].template store_crow<LDV>(sQt[g], tid);
+      ndO[g].template store<LDK>(sdO[g], tid);
+      ndOt[g].template store_crow<LDV>(sdOt[g], tid);
       if (tid < TILE) {
-        sLse[buf][g][tid] = nLse[g];
-        sDb[buf][g][tid] = nDb[g];
+        sLse[g][tid] = nLse[g];
+        sDb[g][tid] = nDb[g];
       }
     }
     if (!has_h0) {
-      nQ[G].template store<LDK>(sQ[buf][G], tid);
-      nQt[G].template store_crow<LDV>(sQt[buf][G], tid);
+      nQ[G].template store<LDK>(sQ[G], tid);
+      nQt[G].template store_crow<LDV>(sQt[G], tid);
     }
   };
 
@@ -1498,13 +1434,6 @@ __global__ __launch_bounds__(NTHREADS, (kv_min_blocks<OP, D, G>())) void bwd_kv_
   // register sets every tile.
   auto sweep = [&](auto h0_tag) {
     constexpr bool H0 = decltype(h0_tag)::value;
-    float hist_next = 0.f;
-    if constexpr (KV_PIPE) {
-      load_tile(NB - 1);
-      hist_next = carry_col[(int64_t)(NB - 1) * T];
-      store_tile(0);
-      __syncthreads();
-    }
 
     // one query tile; INTERIOR: every pair of the tile is unmasked for every wavefront and no key
     // is exempt, so the body is straight-line code without the masks and split products
@@ -1512,21 +1441,11 @@ __global__ __launch_bounds__(NTHREADS, (kv_min_blocks<OP, D, G>())) void bwd_kv_
       constexpr bool INTERIOR = decltype(interior_tag)::value;
       const int qb = NB - 1 - t;
       const int qbase = qb * TILE;
-      const int buf = NBUF == 2 ? (t & 1) : 0;
-      float hist;
-      if constexpr (KV_PIPE) {
-        hist = hist_next;
-        if (t + 1 < ntiles) {
-          load_tile(qb - 1);
-          hist_next = carry_col[(int64_t)(qb - 1) * T];
-        }
-      } else {
-        load_tile(qb);
-        hist = carry_col[(int64_t)qb * T];
-        if (t > 0) __syncthreads();   // every wavefront is done with the previous tile
-        store_tile(0);
-        __syncthreads();
-      }
+      load_tile(qb);
+      const float hist = carry_col[(int64_t)qb * T];
+      if (t > 0) __syncthreads();   // every wavefront is done with the previous tile
+      store_tile();
+      __syncthreads();
       if (INTERIOR || qbase + TILE - 1 >= key0) {   // else every query of the tile precedes every key
         if (h == 0 && j < T) uplane[(int64_t)qb * T + j] = ucarry;
         // tile body; edge: some pair of the tile is masked (diagonal, sequence end) or exempt
@@ -1538,7 +1457,7 @@ __global__ __launch_bounds__(NTHREADS, (kv_min_blocks<OP, D, G>())) void bwd_kv_
         // (a lambda: inlined late, its loop-invariant parts are not hoisted out of the tile loop,
         // which would hold them in registers across it)
         auto body = [&]() {
-          const elem* q0s = H0 ? sQ[buf][0] : sQ[buf][G];
+          const elem* q0s = H0 ? sQ[0] : sQ[G];
           f32x16 l0 = zero16();
   #pragma unroll
           for (int s = 0; s < NS; ++s) l0 = OP::mma(OP::ld_std(q0s, LDK, n, h, s), k0_frag(H0, s), l0);
@@ -1558,14 +1477,14 @@ __global__ __launch_bounds__(NTHREADS, (kv_min_blocks<OP, D, G>())) void bwd_kv_
             } else {
               lg = fs;
   #pragma unroll
-              for (int s = 0; s < NS; ++s) lg = OP::mma(OP::ld_std(sQ[buf][g], LDK, n, h, s), k_frag(g, s), lg);
+              for (int s = 0; s < NS; ++s) lg = OP::mma(OP::ld_std(sQ[g], LDK, n, h, s), k_frag(g, s), lg);
             }
-            f32x16 dp = rows16(sDb[buf][g], h);   // dO.v - dbar
+            f32x16 dp = rows16(sDb[g], h);   // dO.v - dbar
   #pragma unroll
-            for (int s = 0; s < NS; ++s) dp = OP::mma(OP::ld_std(sdO[buf][g], LDK, n, h, s), v_frag(g, s), dp);
+            for (int s = 0; s < NS; ++s) dp = OP::mma(OP::ld_std(sdO[g], LDK, n, h, s), v_frag(g, s), dp);
             f32x16 pr, dz;
-            p_dz_tile<false>(lg, dp, sLse[buf][g], sl2, h, edge, mk, pr, dz);
-            acc_t(dvt[g], sdOt[buf][g], pr, split);
+            p_dz_tile<false>(lg, dp, sLse[g], sl2, h, edge, mk, pr, dz);
+            acc_t(dvt[g], sdOt[g], pr, split);
             if (g == 0) {
               dzsum = dz;
             } else {
@@ -1573,24 +1492,19 @@ __global__ __launch_bounds__(NTHREADS, (kv_min_blocks<OP, D, G>())) void bwd_kv_
               for (int i = 0; i < 16; ++i) dzsum[i] += dz[i];
             }
             if (H0 && g == 0) dz0 = dz;   // head 0's dK waits for g
-            else acc_t(dkt[g], sQt[buf][g], dz, split);
+            else acc_t(dkt[g], sQt[g], dz, split);
           }
           f32x16 gp;
           ucarry = gpath_tile(dzsum, ucarry, gate, h, gp);
           if constexpr (H0) {
   #pragma unroll
             for (int i = 0; i < 16; ++i) dz0[i] += gp[i];
-            acc_t(dkt[0], sQt[buf][0], dz0, true);
+            acc_t(dkt[0], sQt[0], dz0, true);
           } else {
-            acc_t(dk0t, sQt[buf][G], gp, big_tile(gp));
+            acc_t(dk0t, sQt[G], gp, big_tile(gp));
           }
         };
         body();
-      }
-      if constexpr (KV_PIPE) {
-        if constexpr (NBUF == 1) __syncthreads();   // the one buffer is free again
-        if (t + 1 < ntiles) store_tile(NBUF == 2 ? buf ^ 1 : 0);
-        __syncthreads();
       }
     };
     // The last NWAVES tiles hold the wavefronts' diagonals; a workgroup with an exempt key runs
@@ -1655,25 +1569,11 @@ __global__ __launch_bounds__(NTHREADS, (dq_min_blocks<OP, D>())) void bwd_dq_ker
   constexpr int LDZ = TILE + OP::KPAD;
   constexpr int AS = OP::acc_steps;
   constexpr int NH = G + 1;
-  constexpr bool DQ_PIPE = SA_DQ_PIPE != 0;
-  constexpr int TILE_BYTES = (NH * (TILE * LDK + D * LDKT) + G * TILE * LDK) * (int)sizeof(elem);
-  constexpr int NBUF = (DQ_PIPE && SA_DQ_NBUF >= 2 && 2 * TILE_BYTES <= 120 * 1024) ? 2 : 1;
 
-  __shared__ __attribute__((aligned(16))) elem sK[NBUF][NH][TILE * LDK];
-  __shared__ __attribute__((aligned(16))) elem sKt[NBUF][NH][D * LDKT];
-  __shared__ __attribute__((aligned(16))) elem sV[NBUF][G][TILE * LDK];
+  __shared__ __attribute__((aligned(16))) elem sK[NH][TILE * LDK];
+  __shared__ __attribute__((aligned(16))) elem sKt[NH][D * LDKT];
+  __shared__ __attribute__((aligned(16))) elem sV[G][TILE * LDK];
   __shared__ __attribute__((aligned(16))) elem sZ[NWAVES][TILE * LDZ];
-  // the wavefront's row statistics: in registers (SA_DQ_STATREG) or in LDS rows
-  constexpr bool STATREG = SA_DQ_STATREG != 0;
-  __shared__ __attribute__((aligned(16))) float sLse[STATREG ? 1 : NWAVES][G][TILE];
-  __shared__ __attribute__((aligned(16))) float sDb[STATREG ? 1 : NWAVES][G][TILE];
-  // Each wavefront's own Q and dO rows (A operands) stay in registers (with SA_DQ_QLDS, in LDS when
-  // they fit beside the key tiles in half the CU's LDS: an option from when the registers they take
-  // would have cost the second workgroup per CU).
-  constexpr int OTHER_LDS = NBUF * TILE_BYTES + NWAVES * (TILE * LDZ * (int)sizeof(elem) + 2 * G * TILE * 4);
-  constexpr bool QLDS = SA_DQ_QLDS && OTHER_LDS + 2 * NWAVES * G * TILE * LDK * (int)sizeof(elem) <= 80 * 1024;
-  __shared__ __attribute__((aligned(16))) elem sQw[QLDS ? NWAVES : 1][G][QLDS ? TILE * LDK : 8];
-  __shared__ __attribute__((aligned(16))) elem sdOw[QLDS ? NWAVES : 1][G][QLDS ? TILE * LDK : 8];
 
   const int tid = threadIdx.x, lane = tid & 63, wave = wave_id();
   const int n = lane & 31, h = lane >> 5;
@@ -1704,63 +1604,31 @@ __global__ __launch_bounds__(NTHREADS, (dq_min_blocks<OP, D>())) void bwd_dq_ker
   const float* carry_row = carry + ((int64_t)b * NB + qb_c) * T;
   const float* urow = ucheck + (((int64_t)gi * nseq + b) * NB + qb_c) * T;
 
-  // Query-side operands (A operands: lane = query row): the group's Q and dO rows in this
-  // wavefront's LDS, head 0's Q rows in registers.
+  // Query-side operands (A operands: lane = query row): the group's Q and dO rows and head 0's Q
+  // rows in registers, as are the rows' statistics (element i: row crow(i, h)).
   frag q0a[NS];
-  frag qa[QLDS ? 1 : G][NS], doa[QLDS ? 1 : G][NS];
-  if constexpr (!QLDS) {
+  frag qa[G][NS], doa[G][NS];
 #pragma unroll
-    for (int g = 0; g < G; ++g) {
+  for (int g = 0; g < G; ++g) {
 #pragma unroll
-      for (int s = 0; s < NS; ++s) {
-        qa[g][s] = ld_std_bounded<OP>(view_head(q, qs, hd0 + g), view_ld(qs), qbase + n, T, h, s);
-        doa[g][s] = ld_std_bounded<OP>(view_head(dout, dos, hd0 + g), view_ld(dos), qbase + n, T, h, s);
-      }
-    }
-  } else {
-    constexpr int EPC = 16 / (int)sizeof(elem), CPR = D / EPC;
-#pragma unroll
-    for (int g = 0; g < G; ++g) {
-      const elem* qh = view_head(q, qs, hd0 + g);
-      const elem* doh = view_head(dout, dos, hd0 + g);
-      for (int c = lane; c < TILE * CPR; c += 64) {
-        const int r = c / CPR, cc = (c % CPR) * EPC;
-        const int rr = min(qbase + r, T - 1);
-        const bool ok = qbase + r < T;
-        const uint4 xq = *reinterpret_cast<const uint4*>(qh + rr * view_ld(qs) + cc);
-        const uint4 xo = *reinterpret_cast<const uint4*>(doh + rr * view_ld(dos) + cc);
-        *reinterpret_cast<uint4*>(&sQw[wave][g][r * LDK + cc]) =
-            ok ? xq : make_uint4(0u, 0u, 0u, 0u);
-        *reinterpret_cast<uint4*>(&sdOw[wave][g][r * LDK + cc]) =
-            ok ? xo : make_uint4(0u, 0u, 0u, 0u);
-      }
+    for (int s = 0; s < NS; ++s) {
+      qa[g][s] = ld_std_bounded<OP>(view_head(q, qs, hd0 + g), view_ld(qs), qbase + n, T, h, s);
+      doa[g][s] = ld_std_bounded<OP>(view_head(dout, dos, hd0 + g), view_ld(dos), qbase + n, T, h, s);
     }
   }
-  auto q_frag = [&](int g, int s) -> frag {
-    if constexpr (QLDS) return OP::ld_std(sQw[wave][g], LDK, n, h, s);
-    else return qa[g][s];
-  };
-  auto do_frag = [&](int g, int s) -> frag {
-    if constexpr (QLDS) return OP::ld_std(sdOw[wave][g], LDK, n, h, s);
-    else return doa[g][s];
-  };
-  f32x16 lse_r[STATREG ? G : 1], ndb_r[STATREG ? G : 1];
+  auto q_frag = [&](int g, int s) -> frag { return qa[g][s]; };
+  auto do_frag = [&](int g, int s) -> frag { return doa[g][s]; };
+  f32x16 lse_r[G], ndb_r[G];
 #pragma unroll
   for (int g = 0; g < G; ++g) {
     const int64_t row = seq_row + hd0 + g;
-    if constexpr (STATREG) {
 #pragma unroll
-      for (int i = 0; i < 16; ++i) {
-        const int r = qbase + crow(i, h);
-        const int rr = min(r, T - 1);
-        const float lv = lse[row * T + rr], dv_ = dbar[row * T + rr];
-        lse_r[g][i] = (r < T) ? lv : INFINITY;   // rows past the end: P = 0
-        ndb_r[g][i] = (r < T) ? -dv_ : 0.f;     // negated: dO.v accumulates onto it
-      }
-    } else if (lane < TILE) {
-      const int r = qbase + lane;
-      sLse[wave][g][lane] = (r < T) ? lse[row * T + r] : INFINITY;   // rows past the end: P = 0
-      sDb[wave][g][lane] = (r < T) ? -dbar[row * T + r] : 0.f;   // negated: dO.v accumulates onto it
+    for (int i = 0; i < 16; ++i) {
+      const int r = qbase + crow(i, h);
+      const int rr = min(r, T - 1);
+      const float lv = lse[row * T + rr], dv_ = dbar[row * T + rr];
+      lse_r[g][i] = (r < T) ? lv : INFINITY;   // rows past the end: P = 0
+      ndb_r[g][i] = (r < T) ? -dv_ : 0.f;     // negated: dO.v accumulates onto it
     }
   }
   if (!has_h0) {
@@ -1806,16 +1674,16 @@ __global__ __launch_bounds__(NTHREADS, (dq_min_blocks<OP, D>())) void bwd_dq_ker
       nKt[G].load(kt + seq_row * D * ldt, ldt, kbase, tid);
     }
   };
-  auto store_tile = [&](int buf) {
+  auto store_tile = [&]() {
 #pragma unroll
     for (int g = 0; g < G; ++g) {
-      nK[g].template store<LDK>(sK[buf][g], tid);
-      nV[g].template store<LDK>(sV[buf][g], tid);
-      nKt[g].template store<LDKT>(sKt[buf][g], tid);
+      nK[g].template store<LDK>(sK[g], tid);
+      nV[g].template store<LDK>(sV[g], tid);
+      nKt[g].template store<LDKT>(sKt[g], tid);
     }
     if (!has_h0) {
-      nK[G].template store<LDK>(sK[buf][G], tid);
-      nKt[G].template store<LDKT>(sKt[buf][G], tid);
+      nK[G].template store<LDK>(sK[G], tid);
+      nKt[G].template store<LDKT>(sKt[G], tid);
     }
   };
 
@@ -1885,42 +1753,25 @@ __global__ __launch_bounds__(NTHREADS, (dq_min_blocks<OP, D>())) void bwd_dq_ker
   // key side).
   auto sweep = [&](auto h0_tag) {
     constexpr bool H0 = decltype(h0_tag)::value;
-    float hist_next = 0.f, u_next = 0.f;
-    if constexpr (DQ_PIPE) {
-      load_tile(0);
-      key_vals(0, hist_next, u_next);
-      store_tile(0);
-      __syncthreads();
-    }
 
     // one key tile; INTERIOR: no pair of the tile is masked or exempt for any wavefront, so the
     // body is straight-line code without the masks
     auto tile_step = [&](int ktile, auto interior_tag) {
       constexpr bool INTERIOR = decltype(interior_tag)::value;
       const int kbase = ktile * TILE;
-      const int buf = NBUF == 2 ? (ktile & 1) : 0;
       float hist, uin;
-      if constexpr (DQ_PIPE) {
-        hist = hist_next;
-        uin = u_next;
-        if (ktile + 1 < wg_end) {
-          load_tile(ktile + 1);
-          key_vals(ktile + 1, hist_next, u_next);
-        }
-      } else {
-        load_tile(ktile);
-        key_vals(ktile, hist, uin);
-        if (ktile > 0) __syncthreads();   // every wavefront is done with the previous tile
-        store_tile(0);
-        __syncthreads();
-      }
+      load_tile(ktile);
+      key_vals(ktile, hist, uin);
+      if (ktile > 0) __syncthreads();   // every wavefront is done with the previous tile
+      store_tile();
+      __syncthreads();
       if (ktile < my_end) {
         const int j = kbase + n;
         // tile body; edge: some pair of the tile is masked (diagonal, sequence end) or exempt
         const bool edge = !INTERIOR && ((kbase + TILE - 1 >= qbase) || (kbase + TILE > T) || kbase < exempt);
         const TileMasks mk(j, qbase, T, exempt, h);
         {
-          const elem* k0s = H0 ? sK[buf][0] : sK[buf][G];
+          const elem* k0s = H0 ? sK[0] : sK[G];
           f32x16 l0 = zero16();
   #pragma unroll
           for (int s = 0; s < NS; ++s)
@@ -1940,17 +1791,15 @@ __global__ __launch_bounds__(NTHREADS, (dq_min_blocks<OP, D>())) void bwd_dq_ker
               lg = fs;
   #pragma unroll
               for (int s = 0; s < NS; ++s)
-                lg = OP::mma(q_frag(g, s), OP::ld_std(sK[buf][g], LDK, n, h, s), lg);
+                lg = OP::mma(q_frag(g, s), OP::ld_std(sK[g], LDK, n, h, s), lg);
             }
             f32x16 dp;   // dO.v - dbar
-            if constexpr (STATREG) dp = ndb_r[g];
-            else dp = rows16(sDb[wave][g], h);
+            dp = ndb_r[g];
   #pragma unroll
             for (int s = 0; s < NS; ++s)
-              dp = OP::mma(do_frag(g, s), OP::ld_std(sV[buf][g], LDK, n, h, s), dp);
+              dp = OP::mma(do_frag(g, s), OP::ld_std(sV[g], LDK, n, h, s), dp);
             f32x16 pr, dz;
-            if constexpr (STATREG) p_dz_tile_r(lg, dp, lse_r[g], sl2, edge, mk, pr, dz);
-            else p_dz_tile<false>(lg, dp, sLse[wave][g], sl2, h, edge, mk, pr, dz);
+            p_dz_tile_r(lg, dp, lse_r[g], sl2, edge, mk, pr, dz);
             if (g == 0) {
               zsum = dz;
             } else {
@@ -1960,7 +1809,7 @@ __global__ __launch_bounds__(NTHREADS, (dq_min_blocks<OP, D>())) void bwd_dq_ker
             if (H0 && g == 0) {
               dz0 = dz;
             } else {
-              acc_xk(dqacc[g], dz, sKt[buf][g], false);
+              acc_xk(dqacc[g], dz, sKt[g], false);
             }
           }
 
@@ -1970,16 +1819,11 @@ __global__ __launch_bounds__(NTHREADS, (dq_min_blocks<OP, D>())) void bwd_dq_ker
             f32x16 dzh;
   #pragma unroll
             for (int i = 0; i < 16; ++i) dzh[i] = dz0[i] + gp[i];
-            acc_xk(dqacc[0], dzh, sKt[buf][0], true);
+            acc_xk(dqacc[0], dzh, sKt[0], true);
           } else {
-            acc_xk(dq0acc, gp, sKt[buf][G], big_tile(gp));
+            acc_xk(dq0acc, gp, sKt[G], big_tile(gp));
           }
         }
-      }
-      if constexpr (DQ_PIPE) {
-        if constexpr (NBUF == 1) __syncthreads();   // the one buffer is free again
-        if (ktile + 1 < wg_end) store_tile(NBUF == 2 ? buf ^ 1 : 0);
-        __syncthreads();
       }
     };
     // tiles holding exempt keys, then the interior ones (below every wavefront's diagonal, which
@@ -2061,19 +1905,13 @@ __global__ __launch_bounds__(NTHREADS) void bwd_finish_kernel(
 // workspace's state rows; decode_finish_kernel merges the partials and copies the state rows over
 // the caller's state after every head has read the old one (a kernel boundary later).
 
-#ifndef SA_DEC_NR
-#define SA_DEC_NR 8
-#endif
-
-#ifndef SA_DEC_MINB
-#define SA_DEC_MINB 1
-#endif
+constexpr int DEC_NR = 8;   // cached rows of K (and of V) per lane per step, at most
 template <typename E, int D>
 struct DecLayout {
   static constexpr int EPC = 16 / (int)sizeof(E);   // elements per 16-byte load
   static constexpr int LPK = D / EPC;                // lanes per cached row
   static constexpr int KPI = 64 / LPK;               // rows per load instruction
-  static constexpr int NR = LPK < SA_DEC_NR ? LPK : SA_DEC_NR;   // rows per lane per step (K, V each)
+  static constexpr int NR = LPK < DEC_NR ? LPK : DEC_NR;   // rows per lane per step (K, V each)
   static constexpr int DUP = LPK / NR;               // lanes holding one logit after the reduction
   static constexpr int STEP = KPI * NR;              // keys per wavefront step
 };
@@ -2095,7 +1933,7 @@ __device__ __forceinline__ float to_f32(E x) {
 }
 
 template <typename E, int D>
-__global__ __launch_bounds__(NTHREADS, SA_DEC_MINB) void decode_partial_kernel(
+__global__ __launch_bounds__(NTHREADS) void decode_partial_kernel(
     const E* __restrict__ q, const E* __restrict__ k, const E* __restrict__ v, const float* __restrict__ selected,
     int64_t state_ld, float* __restrict__ pm, float* __restrict__ pl, float* __restrict__ po,
     float* __restrict__ next_state, int heads, int groups, int t, int64_t kvs, int exempt, float scale, int chunk,
@@ -2352,7 +2190,7 @@ template <class OP, int D>
 int run_selection(const FwdCall& c, hipStream_t st) {
   using elem = typename OP::elem;
   const int NBq = (int)cdiv(c.Tq, TILE), NKT = (int)cdiv(c.Tk, TILE);
-  const int RB = SA_SEL_RB;
+  const int RB = SEL_RB;
   dim3 g1((unsigned)cdiv(NKT, NWAVES), (unsigned)cdiv(NBq, RB), (unsigned)c.nseq);
   TimedLaunch timed(SA_KERNEL_SELECTION, st);
   hipLaunchKernelGGL((sel_colsum_kernel<OP, D>), g1, dim3(NTHREADS), 0, st, static_cast<const elem*>(c.q),
@@ -2414,8 +2252,9 @@ void launch_kv_from(const KvLaunch& a) {
                      a.scale);
 }
 
+// The two backward kernels; returns the launch status.
 template <class OP, int D, int G>
-void launch_bwd(const BwdCall& c, const typename OP::elem* qt, const typename OP::elem* kt,
+int launch_bwd(const BwdCall& c, const typename OP::elem* qt, const typename OP::elem* kt,
                 const typename OP::elem* dot, const float* lse, const float* dbar, float* ucheck, float* dq0h,
                 float* dk0h, float* dq0x, float* dk0x, int64_t ldt) {
   using elem = typename OP::elem;
@@ -2429,33 +2268,37 @@ void launch_bwd(const BwdCall& c, const typename OP::elem* qt, const typename OP
     return s.row == D && s.head == (int64_t)c.T * D && s.seq == (int64_t)c.H * s.head;
   };
   const bool cv = contiguous(c.qs) && contiguous(c.ks) && contiguous(c.vs) && contiguous(c.dos);
-  // bf16: the key-side kernel's instances live in a translation unit of their own (sa_bf16_kv.hip)
   const int f32 = c.grad_dtype == SA_DTYPE_F32;
   const GradView dqv{c.dq, c.dqs, f32}, dkv{c.dk, c.dks, f32}, dvv{c.dv, c.dvs, f32};
   const KvLaunch kv{q,    k,       v,      qt,   dout, dot,    c.qs, c.ks, c.vs, c.dos,    lse,      dbar,
                     c.carry, ucheck, dk0h, dk0x, dkv,  dvv,    c.nseq, c.H,  c.T,  ldt,      c.exempt, c.scale,
                     c.st};
-#define SA_LAUNCH_KV(CVV)                                                                                         \
-  do {                                                                                                            \
-    if constexpr (sizeof(elem) == 2) launch_bwd_kv_bf16(D, G, CVV, kv);                                          \
-    else launch_kv_from<OP, D, G, CVV>(kv);                                                                       \
-  } while (0)
+  // bf16: the key-side kernel's instances live in a translation unit of their own (sa_bf16_kv.hip)
+  auto launch_kv = [&](bool cvv) -> int {
+    if constexpr (sizeof(elem) == 2) {
+      return launch_bwd_kv_bf16(D, G, cvv, kv);
+    } else {
+      if (cvv) launch_kv_from<OP, D, G, true>(kv);
+      else launch_kv_from<OP, D, G, false>(kv);
+      return launch_status();
+    }
+  };
 #define SA_LAUNCH_DQ(CVV)                                                                                         \
   hipLaunchKernelGGL((bwd_dq_kernel<OP, D, G, CVV>), grid, dim3(NTHREADS), 0, c.st, q, k, v, kt, dout, c.qs, c.ks, \
                      c.vs, c.dos, lse, dbar, c.carry, ucheck, dq0h, dq0x, dqv, c.nseq, c.H, c.T, ldt, c.exempt,   \
                      c.scale)
   {
     TimedLaunch timed(SA_KERNEL_BACKWARD, c.st);
-    if (cv) SA_LAUNCH_KV(true);
-    else SA_LAUNCH_KV(false);
+    const int rc = launch_kv(cv);
+    if (rc) return rc;
   }
   {
     TimedLaunch timed(SA_KERNEL_BACKWARD_DQ, c.st);
     if (cv) SA_LAUNCH_DQ(true);
     else SA_LAUNCH_DQ(false);
   }
-#undef SA_LAUNCH_KV
 #undef SA_LAUNCH_DQ
+  return launch_status();
 }
 
 template <class OP, int D>
@@ -2491,14 +2334,16 @@ int backward_impl(const BwdCall& c) {
                      // and group): cleared here
                      reinterpret_cast<float4*>(dq0x), reinterpret_cast<float4*>(dk0x),
                      (int64_t)nseq * T * D / 4);
+  int rc = launch_status();   // the transposes and row statistics
+  if (rc) return rc;
 #define SA_LAUNCH_BWD(GG) launch_bwd<OP, D, GG>(c, qt, kt, dot, lse, dbar, ucheck, dq0h, dk0h, dq0x, dk0x, ldt)
   if constexpr (sizeof(elem) == 2 && D <= 32) {
-    if (G == 2) SA_LAUNCH_BWD(2);
-    else SA_LAUNCH_BWD(1);
+    rc = (G == 2) ? SA_LAUNCH_BWD(2) : SA_LAUNCH_BWD(1);
   } else {
-    SA_LAUNCH_BWD(1);
+    rc = SA_LAUNCH_BWD(1);
   }
 #undef SA_LAUNCH_BWD
+  if (rc) return rc;
   // head 0's dQ, dK: its own sums plus the other groups' shares
   const int64_t total4 = (int64_t)nseq * T * D / 4;
   const int f32 = c.grad_dtype == SA_DTYPE_F32;
@@ -2510,15 +2355,10 @@ int backward_impl(const BwdCall& c) {
   return launch_status();
 }
 
-#ifndef SA_DEC_CHUNK
-#define SA_DEC_CHUNK 0   // keys per decode workgroup; 0: decode_chunk() picks
-#endif
-
 // Keys per decode workgroup: the smallest power of two from 256 up that keeps the grid at or under
 // 2048 workgroups (8 per CU) up to 4096 keys, and beyond that as far as a row's partials need to
 // fit decode_finish_kernel's LDS.
 inline int decode_chunk(int64_t rows, int64_t t) {
-  if (SA_DEC_CHUNK) return SA_DEC_CHUNK;
   int64_t chunk = 256;
   while ((chunk < 4096 && rows * cdiv(t, chunk) > 2048) || cdiv(t, chunk) > DEC_FIN_MAXPARTS) chunk *= 2;
   return (int)chunk;
