@@ -148,15 +148,16 @@ def tail(q, k, v, tail_len: int, chunk: int = 1024, exempt: int = 1):
     Returns (rows, out_rows, total)."""
     bsz, heads, t, d = q.shape
     start = t - tail_len
-    earlier = torch.zeros(bsz, t, dtype=q.dtype)
+    dev = q.device
+    earlier = torch.zeros(bsz, t, dtype=q.dtype, device=dev)
     for a in range(0, start, chunk):
         e = min(a + chunk, start)
         earlier += selection(q[:, :, a:e], k, exempt, q_offset=a).sum(dim=1)
     sel = selection(q[:, :, start:], k, exempt, q_offset=start)
     hist = earlier[:, None, :] + torch.cumsum(sel, dim=1) - sel
     lg = raw_logits(q[:, :, start:], k) - hist[:, None]
-    rows = torch.arange(start, t)
-    lg = lg.masked_fill(torch.arange(t)[None, None, None, :] > rows[None, None, :, None], float("-inf"))
+    rows = torch.arange(start, t, device=dev)
+    lg = lg.masked_fill(torch.arange(t, device=dev)[None, None, None, :] > rows[None, None, :, None], float("-inf"))
     return rows, lg.softmax(dim=-1) @ v, earlier + sel.sum(dim=1)
 
 

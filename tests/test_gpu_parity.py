@@ -336,7 +336,8 @@ def test_c2_slice_bf16_inputs_bf16_gradients(cuda):
 
 def test_c2_full_length_prefix_is_exact(cuda):
     """At T=16384 (C2's length) the first 2048 rows equal the T=2048 run bit for bit (causality), the
-    selection totals agree with a chunk-summed oracle on the last rows, and the gradients are finite."""
+    last rows and the selection totals agree with the oracle's chunk-summed tail form, and the full
+    backward at that length returns finite gradients in the inputs' dtype."""
     g = torch.Generator().manual_seed(77)
     q, k, v = (torch.randn(1, 16, 16384, 64, generator=g).bfloat16().to(cuda) for _ in range(3))
     full, aux = kernels.selective_attention_forward(q, k, v, return_aux=True)
@@ -348,6 +349,12 @@ def test_c2_full_length_prefix_is_exact(cuda):
     assert (got - want).abs().max().item() < 2e-2
     rel = (aux["selected_total"].cpu() - total).abs().max() / total.abs().max()
     assert rel.item() < 1e-2
+    qq, kk, vv = (t.requires_grad_(True) for t in (q, k, v))
+    out = kernels.selective_attention(qq, kk, vv)
+    torch.testing.assert_close(out.detach(), full, rtol=0, atol=0)
+    out.backward(torch.randn(out.shape, device=cuda, generator=torch.Generator(device=cuda).manual_seed(5)))
+    for t in (qq, kk, vv):
+        assert t.grad.dtype == torch.bfloat16 and torch.isfinite(t.grad).all()
 
 
 def test_c1_fp32_forward_within_1e_4_relative(cuda):
@@ -380,8 +387,8 @@ def test_c5_per_head_slice_bf16_within_2e_2(cuda):
     out = kernels.selective_attention(qq, kk, vv, dot_precision="bf16")
     out.backward(r(do).to(cuda))
     errs = {}
-    for hh in range(0, b * h, 8):   # the oracle per sequence (each one head), 4 of the 32
-        sl = slice(hh, hh + 1)
+    for hh in range(0, b * h, 8):   # the oracle on every sequence (each one head), 8 at a time
+        sl = slice(hh, hh + 8)
         rq, rk, rv = (x[sl].double().requires_grad_(True) for x in (r(q), r(k), r(v)))
         ref = sa_oracle.attention(rq, rk, rv)
         ref.backward(r(do)[sl].double())
