@@ -1,21 +1,25 @@
-"""Benchmark of the Selective Attention operator on one MI355X.
+"""Benchmark of the Selective Attention operator on one MI355X (BASELINE config C2 and the rest).
 
 One step = one fused forward + backward of the operator through the reference's API
 (`selective_attention(q, k, v)` then the gradients of q, k, v for an upstream gradient dO) at
 B=1, H=16, T=16384, D=64 in bf16, inputs already resident in HBM. The step includes everything
 the autograd op launches: the selection scan, the forward, the backward's transposes / row
-statistics / zeroing, the backward kernel and the gradient epilogue.
+statistics, the two backward kernels and the gradient epilogue.
 
-Printed (rank 0, one JSON line): TFLOP/s under the FlashAttention convention (forward 2*B*H*D*T^2,
+Printed (one JSON line): TFLOP/s under the FlashAttention convention (forward 2*B*H*D*T^2,
 forward + backward 7*B*H*D*T^2, causal pairs counted as T^2/2), the roofline of the dominant kernel
-(the longest of the forward, key-side backward and query-side backward kernels: the products it computes
-/ its average HIP-event duration inside the timed region, against the 2.5 PFLOP/s dense bf16 MFMA peak), and a CPU baseline: the fp32 listing (the
-test oracle) timed on this host for a bounded sample of the same workload.
+(the longest of the forward, key-side backward and query-side backward kernels: the products it
+computes / its average HIP-event duration inside the timed region, against the 2.5 PFLOP/s dense
+bf16 MFMA peak), and CPU baselines: the fp32 listing (the test oracle) timed on this host for a
+bounded sample of the C2 workload, and at C1's own shape.
 
-The same line carries the metric's "train tok/s": full training steps of the 24-layer decoder at
-1 x 16384 tokens (the reference's 209M geometry; selective_attention/harness.py, config C3).
+The same line carries BASELINE's other configurations (selective_attention/harness.py):
+  train   C3, full training steps of the 24-layer decoder at 1 x 16384 tokens, both geometries
+          (the reference's 209M d768 / 12 heads, and BASELINE's literal d1024 / 16 heads)
+  c4      C4, the 131072-token prefill in 8 chunks of 16384 through 24 d1024 layers
+  c5      C5, per-head selection fwd+bwd at B=2 H=16 T=32768 D=64 with its dominant kernel's roofline
 
-    python bench.py [--steps K] [--warmup W] [--no-cpu-baseline] [--no-train]
+    python bench.py [--steps K] [--warmup W] [--no-cpu-baseline] [--no-train] [--no-configs]
 """
 
 from __future__ import annotations
@@ -76,15 +80,7 @@ def cpu_baseline(budget_s: float = 20.0) -> dict:
         out = sa_oracle.attention(q, k, v)
         torch.autograd.grad(out, (q, k, v), do)
 
-    run()
-    times = []
-    t_end = time.perf_counter() + budget_s
-    while time.perf_counter() < t_end or len(times) < 3:
-        t0 = time.perf_counter()
-        run()
-        times.append(time.perf_counter() - t0)
-    times.sort()
-    med = times[len(times) // 2]
+    med, reps = _median_time(run, budget_s, 3)
     flop = 7.0 * B * H * D * t * t
     return {
         "value": flop / med / 1e12,
@@ -92,9 +88,49 @@ def cpu_baseline(budget_s: float = 20.0) -> dict:
         "cores": torch.get_num_threads(),
         "kind": "port",
         "sample": (f"fp32 listing (oracle/sa_oracle.py, torch on CPU) fwd+bwd at B=1 H=16 T=2048 D=64, "
-                   f"median of {len(times)} reps = {med * 1e3:.0f} ms; 7*B*H*D*T^2 FLOP; "
+                   f"median of {reps} reps = {med * 1e3:.0f} ms; 7*B*H*D*T^2 FLOP; "
                    f"{len(os.sched_getaffinity(0))} cores visible, CPU {_cpu_model()}"),
     }
+
+
+def cpu_c1(budget_s: float = 8.0) -> dict:
+    """C1 as BASELINE states it: the fp32 listing forward on the host CPU at B=1, H=4, T=512, D=64,
+    q, k, v ~ N(0,1) drawn in that order from one seed; median of >= 10 reps after 2 warm-ups."""
+
+    import torch
+
+    from oracle import sa_oracle
+
+    g = torch.Generator().manual_seed(0)
+    q, k, v = (torch.randn(1, 4, 512, 64, generator=g) for _ in range(3))
+    with torch.no_grad():
+        med, reps = _median_time(lambda: sa_oracle.attention(q, k, v), budget_s, 10, warmup=2)
+    flop = 2.0 * 1 * 4 * 64 * 512 * 512
+    return {"config": "C1: fp32 listing forward on CPU, B=1 H=4 T=512 D=64 (oracle/sa_oracle.py)",
+            "ms": med * 1e3, "reps": reps, "gflops": flop / med / 1e9, "cores": torch.get_num_threads(),
+            "cpu": _cpu_model()}
+
+
+def _median_time(fn, budget_s: float, min_reps: int, warmup: int = 1) -> tuple[float, int]:
+    for _ in range(warmup):
+        fn()
+    times = []
+    t_end = time.perf_counter() + budget_s
+    while time.perf_counter() < t_end or len(times) < min_reps:
+        t0 = time.perf_counter()
+        fn()
+        times.append(time.perf_counter() - t0)
+    times.sort()
+    return times[len(times) // 2], len(times)
+
+
+def _progress(msg: str) -> None:
+    print(f"bench: {msg}", file=sys.stderr, flush=True)
+
+
+def _rounded(d: dict) -> dict:
+    return {k_: (round(v_, 4) if isinstance(v_, float) else (_rounded(v_) if isinstance(v_, dict) else v_))
+            for k_, v_ in d.items()}
 
 
 def main() -> int:
@@ -103,7 +139,8 @@ def main() -> int:
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--no-train", action="store_true", help="skip the 24-layer training-step rate (C3)")
+    ap.add_argument("--no-train", action="store_true", help="skip the 24-layer training-step rates (C3)")
+    ap.add_argument("--no-configs", action="store_true", help="skip the C4 prefill and C5 per-head rates")
     args = ap.parse_args()
     if args.gpus != 1:
         print("bench.py measures one GPU only: the operator runs on a single MI355X "
@@ -175,17 +212,31 @@ def main() -> int:
                      "frac": round(achieved / PEAK_BF16_TFLOPS, 4),
                      "traffic": MEASURED_TRAFFIC_BYTES[dominant], "traffic_unit": "bytes per launch (rocprofv3)"},
     }
-    if not args.no_train:
-        # the metric's "train tok/s": C3, the reference's 209M geometry (d768, 12 heads x 64, 24 layers)
-        del q, k, v, do, grads
-        torch.cuda.empty_cache()
-        from selective_attention import harness
+    del q, k, v, do, grads
+    torch.cuda.empty_cache()
+    _progress(f"C2 {ms:.3f} ms/step")
+    from selective_attention import harness
 
-        tr = harness.train_step_rate("d768", steps=5, warmup=2)
-        record["train_tok_s"] = round(tr["tokens_per_s"], 1)
-        record["train"] = {k_: (round(v_, 3) if isinstance(v_, float) else v_) for k_, v_ in tr.items()}
+    if not args.no_train:
+        # the metric's "train tok/s": C3 at the reference's 209M geometry (d768, 12 heads x 64) and at
+        # BASELINE's literal one (d1024, 16 heads x 64), 24 layers, 1 x 16384 tokens
+        record["train"] = {}
+        for geometry in ("d768", "d1024"):
+            tr = harness.train_step_rate(geometry, steps=10, warmup=3)
+            record["train"][geometry] = _rounded(tr)
+            torch.cuda.empty_cache()
+            _progress(f"C3 {geometry} {tr['tokens_per_s']:.0f} tok/s")
+        record["train_tok_s"] = round(record["train"]["d768"]["tokens_per_s"], 1)
+    if not args.no_configs:
+        record["c4"] = _rounded(harness.prefill_rate(reps=2, warmup=1))
+        torch.cuda.empty_cache()
+        _progress(f"C4 {record['c4']['tokens_per_s']:.0f} tok/s")
+        record["c5"] = _rounded(harness.perhead_rate(steps=5, warmup=2))
+        torch.cuda.empty_cache()
+        _progress(f"C5 {record['c5']['ms_per_step']:.2f} ms/step")
     if not args.no_cpu_baseline:
         record["cpu_baseline"] = cpu_baseline()
+        record["cpu_c1"] = _rounded(cpu_c1())
     print(json.dumps(record), flush=True)
     return 0
 

@@ -63,17 +63,14 @@ def _timed(fn, steps: int, warmup: int) -> float:
 
 
 def model_flop_per_token(cfg: ModelConfig, seq: int) -> float:
-    """Training FLOP per token: 6 N (dense) + the attention products, 7 H D T per layer under the
-    FlashAttention convention (causal pairs T^2/2 counted once, backward 2.5 x forward)."""
-    n = sum(p for p in _param_counts(cfg))
+    """Training FLOP per token: 6 N for the matrix products (every parameter, the tied output head
+    included: its product is real work even though the embedding lookup is not) + the attention
+    products, 7 H D T per layer under the FlashAttention convention (causal pairs T^2/2 counted
+    once, backward 2.5 x forward)."""
+    with torch.device("meta"):
+        n = SelectiveLM(cfg).num_parameters()
     hd = cfg.d_model // cfg.n_heads
     return 6.0 * n + cfg.n_layers * 7.0 * cfg.n_heads * hd * seq
-
-
-def _param_counts(cfg: ModelConfig):
-    with torch.device("meta"):
-        m = SelectiveLM(cfg)
-    yield sum(p.numel() for name, p in m.named_parameters() if "wte" not in name)
 
 
 def train_step_rate(geometry: str = "d768", steps: int = 10, warmup: int = 3, seq: int = 16384, batch: int = 1,
@@ -125,10 +122,16 @@ def prefill_rate(tokens: int = 131072, chunk: int = 16384, geometry: str = "d102
 
     torch.cuda.reset_peak_memory_stats()
     ms = _timed(run, reps, warmup)
+    per_prefill = kernel_times(run, 1, per_call=True)
+    attn_ms = per_prefill["forward"] + per_prefill["selection"]
     hd = cfg.d_model // cfg.n_heads
     attn_flop = layers * 2.0 * cfg.n_heads * hd * tokens * tokens
     return {"config": f"C4 prefill, {geometry}, {layers} layers, {tokens} tokens in chunks of {chunk}, bf16",
-            "tokens_per_s": tokens / (ms * 1e-3), "ms": ms, "attention_tflops": attn_flop / (ms * 1e-3) / 1e12,
+            "tokens_per_s": tokens / (ms * 1e-3), "ms": ms,
+            "attention_kernel_ms": attn_ms, "attention_share": attn_ms / ms,
+            "attention_tflops": attn_flop / (attn_ms * 1e-3) / 1e12,
+            "attention_frac_of_peak": attn_flop / (attn_ms * 1e-3) / 1e12 / PEAK_BF16_TFLOPS,
+            "per_layer_chunk_forward_ms": per_prefill["forward"] / (layers * ((tokens + chunk - 1) // chunk)),
             "peak_mem_gib": torch.cuda.max_memory_allocated() / 2**30}
 
 
@@ -150,10 +153,43 @@ def perhead_rate(batch: int = 2, heads: int = 16, seq: int = 32768, head_dim: in
         torch.autograd.grad(out, (qq, kk, vv), dd)
 
     ms = _timed(step, steps, warmup)
-    flop = 7.0 * batch * heads * head_dim * seq * seq
+    kernel_ms = kernel_times(step, steps)
+    unit = batch * heads * head_dim * seq * seq   # one causal product over all heads
+    flop = 7.0 * unit
     tf = flop / (ms * 1e-3) / 1e12
+    dominant = max(KERNEL_PRODUCTS, key=lambda name: kernel_ms[name])
+    achieved = KERNEL_PRODUCTS[dominant] * unit / (kernel_ms[dominant] * 1e-3) / 1e12
     return {"config": f"C5 per-head fwd+bwd, B={batch} H={heads} T={seq} D={head_dim} bf16, k x2 on 10% of keys",
-            "ms_per_step": ms, "tflops": tf, "frac_of_peak": tf / PEAK_BF16_TFLOPS}
+            "ms_per_step": ms, "tflops": tf, "frac_of_peak": tf / PEAK_BF16_TFLOPS,
+            "kernel_ms": kernel_ms,
+            "roofline": {"bound": "mfma", "kernel": f"{dominant} ({KERNEL_PRODUCTS[dominant]:.0f}*B*H*D*T^2 FLOP)",
+                         "achieved": achieved, "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
+                         "frac": achieved / PEAK_BF16_TFLOPS}}
+
+
+# Products each timed kernel computes (recomputation included), in units of one causal product over
+# all heads (B H D T^2 FLOP): the forward QK^T and PV; the key-side backward QK^T, dO V^T, P^T dO,
+# dz^T Q; the query-side backward QK^T, dO V^T, dz K.
+KERNEL_PRODUCTS = {"forward": 2.0, "backward_kv": 4.0, "backward_dq": 3.0}
+_KERNEL_IDS = {"forward": _lib.KERNEL_FORWARD, "backward_kv": _lib.KERNEL_BACKWARD,
+               "backward_dq": _lib.KERNEL_BACKWARD_DQ, "selection": _lib.KERNEL_SELECTION}
+
+
+def kernel_times(fn, calls: int, per_call: bool = False) -> dict:
+    """Milliseconds of the library's main kernels over `calls` calls of fn(), from the HIP events the
+    library records on each launch's own stream (sa_timing_*): the average per launch, or with
+    per_call the summed time of each kernel per call of fn()."""
+    torch.cuda.synchronize()
+    _lib.timing_enable(True)
+    for _ in range(calls):
+        fn()
+    torch.cuda.synchronize()
+    res = {}
+    for name, kid in _KERNEL_IDS.items():
+        total, n = _lib.timing_read(kid)
+        res[name] = total / calls if per_call else total / max(n, 1)
+    _lib.timing_enable(False)
+    return res
 
 
 def decode_rate(t: int = 131072, batch: int = 1, heads: int = 16, head_dim: int = 64, steps: int = 50,

@@ -164,3 +164,34 @@ def test_api_checks_on_cpu_tensors():
         kernels._damp_mode("linear", 0)
     with pytest.raises(ValueError, match="multiples"):
         kernels._check_blocks(48, 32)
+
+
+def test_custom_ops_have_fake_shape_functions():
+    """The C-ABI calls are torch.library custom ops whose fake (meta) kernels give the shapes and
+    dtypes torch.compile traces with; no GPU is needed to run them."""
+    from torch._subclasses.fake_tensor import FakeTensorMode
+
+    ops = torch.ops.selective_attention
+    with FakeTensorMode():
+        q = torch.empty(2, 4, 100, 32, dtype=torch.bfloat16, device="meta")
+        out, rmax, rden, carry, total = ops.forward(q, q, q, 0.125, 1, 0, 0, 0)
+        assert out.shape == (2, 4, 100, 32) and out.dtype == torch.float32
+        assert rmax.shape == rden.shape == (2, 4, 100) and carry.shape == (2, 4, 100) and total.shape == (2, 100)
+        for flag, dt in ((True, torch.bfloat16), (False, torch.float32)):
+            grads = ops.backward(q, q, q, out, q, rmax, rden, carry, 0.125, 1, 0, flag)
+            assert all(g.shape == q.shape and g.dtype == dt for g in grads)
+        qkv = torch.empty(2, 70, 3 * 4 * 64, dtype=torch.bfloat16, device="meta")
+        y, o, m, d, c = ops.qkv_forward(qkv, 4, 1)
+        assert y.shape == (2, 70, 256) and y.dtype == torch.bfloat16 and o.shape == (2, 4, 70, 64)
+        assert c.shape == (2, 3, 70)
+        assert ops.qkv_backward(qkv, y, o, m, d, c, 4, 1).shape == qkv.shape
+
+
+def test_packed_form_stays_within_32_bit_row_offsets():
+    """One head's rows of the packed projection are addressed with 32-bit byte offsets at the packed
+    row stride 3 * H * D: past 2 GiB the fused form is refused, so the slot takes the split-heads
+    path (rows D apart), which runs ~3 H times longer sequences."""
+    c3 = 3 * 1024   # d1024 / 16 heads
+    assert kernels._packed_rows_fit(300_000, c3, 2)
+    assert not kernels._packed_rows_fit(350_000, c3, 2)   # (T + 64) * 3072 * 2 bytes >= 2^31
+    assert not kernels._packed_rows_fit(175_000, c3, 4)

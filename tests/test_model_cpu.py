@@ -1,6 +1,6 @@
 """The decoder harness and the SelectiveAttention slot on the CPU (reference tests/test_selective_model.py,
-tests/test_selective_perhead.py). The layers run the plain listing here (use_kernel = False, the
-explicit opt-in); the kernel path of the same layers is tested on the GPU (test_model_gpu.py)."""
+tests/test_selective_perhead.py). On CPU tensors the layers run the plain listing, as the reference's
+do; the kernel path of the same layers is tested on the GPU (test_model_gpu.py)."""
 
 from __future__ import annotations
 
@@ -56,8 +56,8 @@ def test_layer_matches_the_oracle():
     model = _tiny()
     layer = model.transformer.h[0].attn
     x = torch.randn(2, 30, 64, dtype=torch.float64)
-    q, k, v = layer._split_heads(x)
-    want = layer._merge_heads(sa_oracle.attention(q, k, v), 2, 30)
+    q, k, v = layer.project(x)
+    want = layer.emit(sa_oracle.attention(q, k, v))
     torch.testing.assert_close(layer(x), want)
 
 
@@ -89,16 +89,50 @@ def test_per_head_layer_is_each_head_alone():
     model = _tiny("selective_perhead")
     layer = model.transformer.h[0].attn
     x = torch.randn(1, 20, 64, dtype=torch.float64)
-    q, k, v = layer._split_heads(x)
+    q, k, v = layer.project(x)
     torch.testing.assert_close(layer._attend(q, k, v)[0], sa_oracle.per_head(q, k, v))
 
 
-def test_kernel_layers_refuse_cpu_tensors():
-    """No silent fallback: with use_kernel on, a CPU input is an error, not the listing."""
-    model = _tiny()
-    model.transformer.h[0].attn.use_kernel = True
-    with pytest.raises((ValueError, RuntimeError)):
-        model(torch.randint(0, 97, (1, 8)))
+def test_cpu_tensors_route_to_the_listing():
+    """With use_kernel on (the default), CPU tensors run the listing, as in the reference
+    (mixers.py:73-74, 87-98): the same outputs and gradients as use_kernel = False."""
+    torch.manual_seed(4)
+    idx = torch.randint(0, 97, (2, 33))
+    on, off = _tiny(), _tiny()
+    for block in on.transformer.h:
+        block.attn.use_kernel = True
+    on.train(), off.train()
+    _, l_on = on(idx[:, :-1], idx[:, 1:])
+    _, l_off = off(idx[:, :-1], idx[:, 1:])
+    l_on.backward(), l_off.backward()
+    torch.testing.assert_close(l_on, l_off, rtol=0, atol=0)
+    for (name, a), (_, b) in zip(on.named_parameters(), off.named_parameters()):
+        torch.testing.assert_close(a.grad, b.grad, rtol=0, atol=0, msg=lambda m: f"{name}: {m}")
+
+
+@pytest.mark.parametrize("attention,chunk", [("selective", 7), ("selective_perhead", 16), ("selective_x16", 5)])
+def test_chunked_prefill_equals_single_shot_on_cpu(attention, chunk):
+    """prefill_chunked (each layer's K/V and selection state carried between chunks) == prefill,
+    on the listing's chunk form."""
+    model = _tiny(attention)
+    idx = torch.randint(0, 97, (2, 37))
+    with torch.no_grad():
+        a, ca = model.prefill(idx, capacity=40)
+        b, cb = model.prefill_chunked(idx, chunk, capacity=40)
+        torch.testing.assert_close(a, b)
+        for x, y in zip(ca, cb):
+            torch.testing.assert_close(x["selected"][:, :, :37], y["selected"][:, :, :37])
+        torch.testing.assert_close(model.decode_step(idx[:, -1:], 37, ca), model.decode_step(idx[:, -1:], 37, cb))
+
+
+def test_registry_factories_build_the_variants():
+    cfg = ModelConfig(vocab_size=50, n_layers=1, d_model=64, n_heads=4, context_length=32)
+    layers = {name: make(cfg) for name, make in mixers.MIXER_CLASSES.items()}
+    assert (layers["selective"].exempt, layers["selective"].groups) == (1, 1)
+    assert (layers["selective_x16"].exempt, layers["selective_x16"].groups) == (16, 1)
+    assert (layers["selective_perhead"].exempt, layers["selective_perhead"].groups) == (1, 4)
+    with pytest.raises(ValueError, match="swiglu"):
+        ModelConfig(mlp="gelu")
 
 
 def test_training_loss_and_backward_on_cpu_listing():
