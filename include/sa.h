@@ -46,6 +46,7 @@ extern "C" {
 #define SA_ERR_DTYPE -3         /* dtype code unknown */
 #define SA_ERR_WORKSPACE -4     /* workspace smaller than the *_workspace_bytes figure */
 #define SA_ERR_LAUNCH -5        /* a kernel launch failed (hipGetLastError) */
+#define SA_ERR_SCRATCH -6       /* sa_decode_noalloc: the step needs more than its fixed scratch */
 
 /* ABI revision of this header; bumps when a signature changes or an entry point is added. */
 int sa_abi_version(void);
@@ -201,6 +202,24 @@ int64_t sa_decode_workspace_bytes(int64_t nseq, int64_t heads, int64_t t, int64_
 int sa_decode(const void* q, const void* k, const void* v, float* out, float* selected, int64_t state_ld,
               void* workspace, int64_t workspace_bytes, int64_t nseq, int64_t heads, int64_t groups, int64_t t,
               int64_t kv_stride, int64_t head_dim, float scale, int dtype, int exempt, void* stream);
+
+/*
+ * sa_decode without a workspace: the same step, arguments (less the workspace pair), results and
+ * errors, for callers that cannot allocate device memory (code under HIP graph capture, tight
+ * serving loops, harnesses that forbid hipMalloc). No counterpart in the reference. It allocates
+ * nothing and records no timing events: the step's scratch (sa_decode_workspace_bytes of it) lives
+ * in a fixed device array of SA_DECODE_SCRATCH_BYTES that the library holds on every GPU it runs
+ * on until the process ends; a step needing more returns SA_ERR_SCRATCH (64 MiB takes, e.g.,
+ * t = 800K keys at nseq 1, heads 16, head_dim 64, or t = 100K at nseq 8). The first call on a
+ * device looks up the array's address there (with that device current). Nothing in the array
+ * needs to start at zero. Every call on one GPU shares that GPU's array, which keeps the last
+ * call's contents: calls that overlap on one GPU (on different streams, or from threads without
+ * ordering between them) race; calls in order on one stream do not.
+ */
+#define SA_DECODE_SCRATCH_BYTES ((int64_t)64 << 20)
+int sa_decode_noalloc(const void* q, const void* k, const void* v, float* out, float* selected, int64_t state_ld,
+                      int64_t nseq, int64_t heads, int64_t groups, int64_t t, int64_t kv_stride, int64_t head_dim,
+                      float scale, int dtype, int exempt, void* stream);
 
 #ifdef __cplusplus
 }

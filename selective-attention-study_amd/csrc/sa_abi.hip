@@ -21,7 +21,7 @@ using namespace sa_host;
 
 extern "C" {
 
-int sa_abi_version(void) { return 4; }
+int sa_abi_version(void) { return 5; }
 
 int sa_timing_enable(int on) {
   TimingRegistry& r = timing();
@@ -61,6 +61,7 @@ const char* sa_status_string(int status) {
     case SA_ERR_DTYPE: return "unknown dtype code";
     case SA_ERR_WORKSPACE: return "workspace too small";
     case SA_ERR_LAUNCH: return "HIP kernel launch failed";
+    case SA_ERR_SCRATCH: return "the decode step needs more scratch than sa_decode_noalloc's fixed array holds";
     default: return "unknown status";
   }
 }
@@ -233,22 +234,93 @@ int64_t sa_decode_workspace_bytes(int64_t nseq, int64_t heads, int64_t t, int64_
   return decode_workspace_bytes(nseq, heads, t, head_dim);
 }
 
-int sa_decode(const void* q, const void* k, const void* v, float* out, float* selected, int64_t state_ld,
-              void* workspace, int64_t workspace_bytes, int64_t nseq, int64_t heads, int64_t groups, int64_t t,
-              int64_t kv_stride, int64_t head_dim, float scale, int dtype, int exempt, void* stream) {
+// Argument checks of the decode step, shared by sa_decode and sa_decode_noalloc (all but the
+// workspace); kv_stride 0 becomes t * head_dim.
+static int decode_check(const void* q, const void* k, const void* v, const float* out, const float* selected,
+                        int64_t state_ld, int64_t nseq, int64_t heads, int64_t groups, int64_t t,
+                        int64_t& kv_stride, int64_t head_dim, float scale, int dtype, int exempt) {
   if (!valid_dims(nseq, heads, t) || groups < 1 || heads % groups != 0 || exempt < 1) return SA_ERR_ARGUMENT;
-  if (!q || !k || !v || !out || !selected || !workspace || state_ld < t) return SA_ERR_ARGUMENT;
+  if (!q || !k || !v || !out || !selected || state_ld < t) return SA_ERR_ARGUMENT;
   if (!(scale > 0.f) || !(scale < INFINITY)) return SA_ERR_ARGUMENT;
   if (dtype != SA_DTYPE_BF16 && dtype != SA_DTYPE_F32) return SA_ERR_DTYPE;
   if (head_dim != 32 && head_dim != 64 && head_dim != 128) return SA_ERR_HEAD_DIM;
   if (!rows_fit(t, head_dim, dtype)) return SA_ERR_ARGUMENT;
   if (kv_stride == 0) kv_stride = t * head_dim;
   if (kv_stride < t * head_dim || kv_stride % 8 != 0) return SA_ERR_ARGUMENT;
-  if (workspace_bytes < sa_decode_workspace_bytes(nseq, heads, t, head_dim)) return SA_ERR_WORKSPACE;
-  const DecCall c{q,         k,          v,           out,    selected,  state_ld, workspace,
-                  (int)nseq, (int)heads, (int)groups, (int)t, kv_stride, scale,    exempt,
-                  (int)head_dim, static_cast<hipStream_t>(stream)};
+  return SA_OK;
+}
+
+static int decode_run(const void* q, const void* k, const void* v, float* out, float* selected, int64_t state_ld,
+                      void* workspace, int64_t nseq, int64_t heads, int64_t groups, int64_t t, int64_t kv_stride,
+                      int64_t head_dim, float scale, int dtype, int exempt, void* stream, bool timed) {
+  DecCall c{q,         k,          v,           out,    selected,  state_ld, workspace,
+            (int)nseq, (int)heads, (int)groups, (int)t, kv_stride, scale,    exempt,
+            (int)head_dim, static_cast<hipStream_t>(stream)};
+  c.timed = timed;
   return dtype == SA_DTYPE_BF16 ? decode_bf16(c) : decode_f32(c);
+}
+
+int sa_decode(const void* q, const void* k, const void* v, float* out, float* selected, int64_t state_ld,
+              void* workspace, int64_t workspace_bytes, int64_t nseq, int64_t heads, int64_t groups, int64_t t,
+              int64_t kv_stride, int64_t head_dim, float scale, int dtype, int exempt, void* stream) {
+  const int rc = decode_check(q, k, v, out, selected, state_ld, nseq, heads, groups, t, kv_stride, head_dim, scale,
+                              dtype, exempt);
+  if (rc != SA_OK) return rc;
+  if (!workspace) return SA_ERR_ARGUMENT;
+  if (workspace_bytes < sa_decode_workspace_bytes(nseq, heads, t, head_dim)) return SA_ERR_WORKSPACE;
+  return decode_run(q, k, v, out, selected, state_ld, workspace, nseq, heads, groups, t, kv_stride, head_dim, scale,
+                    dtype, exempt, stream, true);
+}
+
+}  // extern "C"
+
+// ---------------------------------------------------------------------------------------------
+// Allocation-free decode: the step's scratch (partial softmax sums, the new state rows) lives in
+// a file-scope device array instead of a workspace argument. Every GPU the library runs on holds
+// its own copy of the array (at its own address) until the process ends. The host-side symbol
+// `scratch` is not a device address: its address on a device comes from hipGetSymbolAddress, once
+// per device with that device current, and only that address reaches kernels.
+
+static __device__ __align__(256) unsigned char scratch[SA_DECODE_SCRATCH_BYTES];
+
+namespace {
+
+constexpr int MAX_DEVICES = 64;
+std::mutex scratch_mu;
+void* scratch_at[MAX_DEVICES];   // the array's address on each device, once looked up
+
+// The array's address on the current device, looked up on the first call for that device.
+int scratch_of_current_device(void** out) {
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= MAX_DEVICES) return SA_ERR_LAUNCH;
+  std::lock_guard<std::mutex> lock(scratch_mu);
+  if (!scratch_at[dev]) {
+    void* p = nullptr;
+    if (hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)) != hipSuccess || !p) return SA_ERR_LAUNCH;
+    scratch_at[dev] = p;
+  }
+  *out = scratch_at[dev];
+  return SA_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int sa_decode_noalloc(const void* q, const void* k, const void* v, float* out, float* selected, int64_t state_ld,
+                      int64_t nseq, int64_t heads, int64_t groups, int64_t t, int64_t kv_stride, int64_t head_dim,
+                      float scale, int dtype, int exempt, void* stream) {
+  const int rc = decode_check(q, k, v, out, selected, state_ld, nseq, heads, groups, t, kv_stride, head_dim, scale,
+                              dtype, exempt);
+  if (rc != SA_OK) return rc;
+  if (sa_decode_workspace_bytes(nseq, heads, t, head_dim) > SA_DECODE_SCRATCH_BYTES) return SA_ERR_SCRATCH;
+  void* ws = nullptr;
+  const int got = scratch_of_current_device(&ws);
+  if (got != SA_OK) return got;
+  // nothing in the scratch needs to start at zero: the partial kernel writes every partial and
+  // state row the finishing kernel reads
+  return decode_run(q, k, v, out, selected, state_ld, ws, nseq, heads, groups, t, kv_stride, head_dim, scale, dtype,
+                    exempt, stream, false);
 }
 
 }  // extern "C"

@@ -32,10 +32,12 @@ struct TimingRegistry {
 };
 TimingRegistry& timing();   // the one registry (sa_abi.hip)
 
-// Brackets one launch: construct before it, destroy after it (both on stream st).
+// Brackets one launch: construct before it, destroy after it (both on stream st). A negative
+// kernel id records nothing (callers that must not create events).
 class TimedLaunch {
  public:
   TimedLaunch(int kernel, hipStream_t st) : kernel_(kernel), st_(st) {
+    if (kernel_ < 0) return;
     TimingRegistry& r = timing();
     std::lock_guard<std::mutex> lock(r.mu);
     if (!r.on) return;
@@ -195,6 +197,7 @@ struct DecCall {
   float scale;
   int exempt, head_dim;
   hipStream_t st;
+  bool timed = true;   // false: no timing events (the allocation-free entry point)
 };
 
 // Workspace of sa_decode: the partials of (nseq*heads, chunks of 256 keys or more) fp32 maxima,

@@ -2380,7 +2380,7 @@ int decode_impl(const DecCall& c) {
   float* next_state = pm + decode_partials_floats(c.nseq, c.heads, c.t, D);
   dim3 g1((unsigned)nchunk, (unsigned)rows);
   {
-    TimedLaunch timed(SA_KERNEL_DECODE, c.st);
+    TimedLaunch timed(c.timed ? SA_KERNEL_DECODE : -1, c.st);
     hipLaunchKernelGGL((decode_partial_kernel<elem, D>), g1, dim3(NTHREADS), 0, c.st, static_cast<const elem*>(c.q),
                        static_cast<const elem*>(c.k), static_cast<const elem*>(c.v), c.selected, c.state_ld, pm, pl,
                        po, next_state, c.heads, c.groups, c.t, c.kvs, c.exempt, c.scale, chunk, nchunk);

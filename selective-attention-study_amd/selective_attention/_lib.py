@@ -56,7 +56,11 @@ SIGNATURES = {
                          _I64, _I64, _I64, _I64, _F, _I, _I, _I, _I, _P]),
     "sa_decode_workspace_bytes": (_I64, [_I64, _I64, _I64, _I64]),
     "sa_decode": (_I, [_P, _P, _P, _P, _P, _I64, _P, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _F, _I, _I, _P]),
+    "sa_decode_noalloc": (_I, [_P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _F, _I, _I, _P]),
 }
+
+# Bytes of the fixed device scratch of sa_decode_noalloc (SA_DECODE_SCRATCH_BYTES).
+DECODE_SCRATCH_BYTES = 64 << 20
 
 _lock = threading.Lock()
 _lib = None

@@ -35,7 +35,7 @@ def test_library_loads_and_exports_every_declared_symbol():
 
 def test_status_strings():
     lib = _lib.load()
-    for code in (0, -1, -2, -3, -4, -5):
+    for code in (0, -1, -2, -3, -4, -5, -6):
         assert lib.sa_status_string(code)
     assert b"head_dim" in lib.sa_status_string(-2)
 
@@ -75,6 +75,28 @@ def test_decode_rejects_invalid_arguments():
     bad = list(args)
     bad[16] = 0          # exempt
     assert lib.sa_decode(*bad) == -1
+
+
+def test_decode_noalloc_rejects_before_touching_a_device():
+    """The allocation-free decode checks its arguments as sa_decode does, and refuses a step whose
+    scratch exceeds its fixed array, before any device call."""
+    lib = _lib.load()
+    fake = 1 << 20
+    args = [fake] * 5 + [128, 1, 4, 1, 100, 0, 64, 0.125, 0, 1, None]
+    bad = list(args)
+    bad[8] = 3           # groups does not divide heads
+    assert lib.sa_decode_noalloc(*bad) == -1
+    bad = list(args)
+    bad[11] = 48         # head_dim
+    assert lib.sa_decode_noalloc(*bad) == -2
+    bad = list(args)
+    bad[13] = 9          # dtype
+    assert lib.sa_decode_noalloc(*bad) == -3
+    t = 1 << 21          # 2M keys at 16 heads: about 160 MiB of scratch
+    assert lib.sa_decode_workspace_bytes(1, 16, t, 64) > _lib.DECODE_SCRATCH_BYTES
+    big = [fake] * 5 + [t, 1, 16, 1, t, 0, 64, 0.125, 0, 1, None]
+    assert lib.sa_decode_noalloc(*big) == -6
+    assert b"scratch" in lib.sa_status_string(-6)
 
 
 def test_invalid_arguments_are_rejected_before_any_launch():
