@@ -99,9 +99,14 @@ struct BwdLayout {
   int64_t qt, dot, kt, lse, dbar, dq, dk, dq0x, dk0x, ucheck, total;
 };
 
+// Floats of one selection-suffix checkpoint plane: query block qb holds the keys of its causal
+// part, [0, (qb + 1) * TILE), and the rows lie end to end (row qb at utri_row(qb)).
+__host__ __device__ inline int64_t utri_row(int64_t qb) { return (TILE / 2) * qb * (qb + 1); }
+__host__ __device__ inline int64_t utri_floats(int64_t NB) { return utri_row(NB); }
+
 // Workspace of sa_backward: transposed Q, dO, K; row statistics; head 0's fp32 dQ, dK sums and
 // its shares from the other groups (every other gradient goes straight to the caller's views);
-// the selection-suffix checkpoints (one plane per head group).
+// the selection-suffix checkpoints (one lower-triangular plane per head group and sequence).
 inline BwdLayout bwd_layout(int64_t nseq, int64_t heads, int64_t t, int64_t D, int64_t esize, int64_t G) {
   const int64_t R = nseq * heads, ldt = sa_transposed_ld(t), NB = (t + TILE - 1) / TILE;
   BwdLayout L;
@@ -116,7 +121,7 @@ inline BwdLayout bwd_layout(int64_t nseq, int64_t heads, int64_t t, int64_t D, i
   L.dk = take(nseq * t * D * 4);
   L.dq0x = take(nseq * t * D * 4);
   L.dk0x = take(nseq * t * D * 4);
-  L.ucheck = take((heads / G) * nseq * NB * t * 4);
+  L.ucheck = take((heads / G) * nseq * utri_floats(NB) * 4);
   L.total = off;
   return L;
 }

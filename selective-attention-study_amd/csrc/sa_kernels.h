@@ -1266,7 +1266,7 @@ __global__ __launch_bounds__(NTHREADS, (kv_min_blocks<OP, D, G>())) void bwd_kv_
     if constexpr (CV) return D;
     else return vs_.row;
   };
-  float* uplane = ucheck + ((int64_t)gi * nseq + b) * NB * (int64_t)T;
+  float* uplane = ucheck + ((int64_t)gi * nseq + b) * utri_floats(NB);
   const float* carry_col = carry + (int64_t)b * NB * T + (j < T ? j : 0);
 
   // Key-side operands (B operands: lane = key column): this wavefront's K and V rows of the group
@@ -1447,7 +1447,7 @@ __global__ __launch_bounds__(NTHREADS, (kv_min_blocks<OP, D, G>())) void bwd_kv_
       store_tile();
       __syncthreads();
       if (INTERIOR || qbase + TILE - 1 >= key0) {   // else every query of the tile precedes every key
-        if (h == 0 && j < T) uplane[(int64_t)qb * T + j] = ucarry;
+        if (h == 0 && j < T) uplane[utri_row(qb) + j] = ucarry;   // j < (qb + 1) * TILE here
         // tile body; edge: some pair of the tile is masked (diagonal, sequence end) or exempt
         // (rows past the end and keys past the end need no mask on the key side: the latter's sums
         // stay in their own lanes, which are never written)
@@ -1602,7 +1602,9 @@ __global__ __launch_bounds__(NTHREADS, (dq_min_blocks<OP, D>())) void bwd_dq_ker
   // this wavefront's rows of the carry and U checkpoints (key offset added per tile)
   const int qb_c = qb < NB ? qb : NB - 1;
   const float* carry_row = carry + ((int64_t)b * NB + qb_c) * T;
-  const float* urow = ucheck + (((int64_t)gi * nseq + b) * NB + qb_c) * T;
+  // (the row's keys end at (qb_c + 1) * TILE; the tiles past a wavefront's diagonal read, unused,
+  // into the next row, and the last row spans every key tile: the reads stay inside the plane)
+  const float* urow = ucheck + ((int64_t)gi * nseq + b) * utri_floats(NB) + utri_row(qb_c);
 
   // Query-side operands (A operands: lane = query row): the group's Q and dO rows and head 0's Q
   // rows in registers, as are the rows' statistics (element i: row crow(i, h)).
