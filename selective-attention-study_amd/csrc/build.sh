@@ -23,17 +23,31 @@ trap 'rm -rf "$tmp"' EXIT
 common=(--offload-arch=gfx950 -O3 -std=c++17 -fPIC -munsafe-fp-atomics
         -Xclang -target-feature -Xclang -packed-fp32-ops -I"$root/include" "$@")
 
-hipcc "${common[@]}" -mllvm -amdgpu-mfma-vgpr-form -mllvm -amdgpu-sched-strategy=iterative-ilp \
-  -c "$here/sa_bf16.hip" -o "$tmp/sa_bf16.o" &
+# unit <source> <object> [compiler-internal options...]: the options (-mllvm ...) are this compiler's
+# internal knobs, not a stable interface; if a compiler release drops or rejects them the unit is
+# compiled again without them (correct code, slower tile loops) and the build says so.
+unit() {
+  local src=$1 obj=$2
+  shift 2
+  if hipcc "${common[@]}" "$@" -c "$here/$src" -o "$tmp/$obj" 2> "$tmp/$obj.err"; then
+    grep -v "packed-fp32-ops" "$tmp/$obj.err" >&2 || true
+    return 0
+  fi
+  if [ $# -eq 0 ]; then cat "$tmp/$obj.err" >&2; return 1; fi
+  echo "build.sh: $src failed with the internal options ($*); compiling it without them" >&2
+  hipcc "${common[@]}" -c "$here/$src" -o "$tmp/$obj"
+}
+
+tuned=(-mllvm -amdgpu-mfma-vgpr-form -mllvm -amdgpu-sched-strategy=iterative-ilp)
+unit sa_bf16.hip sa_bf16.o "${tuned[@]}" &
 p1=$!
-hipcc "${common[@]}" -mllvm -amdgpu-mfma-vgpr-form -mllvm -amdgpu-sched-strategy=iterative-ilp \
-  -c "$here/sa_bf16_kv.hip" -o "$tmp/sa_bf16_kv.o" &
+unit sa_bf16_kv.hip sa_bf16_kv.o "${tuned[@]}" &
 p4=$!
-hipcc "${common[@]}" -mllvm -amdgpu-mfma-vgpr-form -c "$here/sa_bf16_dec.hip" -o "$tmp/sa_bf16_dec.o" &
+unit sa_bf16_dec.hip sa_bf16_dec.o -mllvm -amdgpu-mfma-vgpr-form &
 p5=$!
-hipcc "${common[@]}" -c "$here/sa_f32.hip" -o "$tmp/sa_f32.o" &
+unit sa_f32.hip sa_f32.o &
 p2=$!
-hipcc "${common[@]}" -c "$here/sa_abi.hip" -o "$tmp/sa_abi.o" &
+unit sa_abi.hip sa_abi.o &
 p3=$!
 rc=0
 wait $p1 || rc=1

@@ -68,6 +68,19 @@ def test_forward_head_dims(cuda, head_dim, heads):
     _close(got.cpu(), sa_oracle.attention(q.double(), k.double(), v.double()), 2e-5, 2e-5, "out")
 
 
+@pytest.mark.parametrize("head_dim", [32, 64, 128])
+@pytest.mark.parametrize("blocks", [(32, 32), (64, 32), (128, 64), (None, 128)])
+def test_forward_block_shapes(cuda, head_dim, blocks):
+    """The reference's launch-policy arguments (block_m, block_n, num_stages; reference
+    tests/test_selective_kernels.py:100-105) are accepted and validated; the HIP kernels tile by
+    their own policy, so every choice returns the oracle's outputs."""
+    print(f"case forward blocks={blocks} head_dim={head_dim}", flush=True)
+    q, k, v = _qkv(1, 2, 300, head_dim, seed=head_dim, scale=1.5)
+    got = kernels.selective_attention_forward(q.to(cuda), k.to(cuda), v.to(cuda), dot_precision="ieee",
+                                              block_m=blocks[0], block_n=blocks[1], num_stages=1)
+    _close(got.cpu(), sa_oracle.attention(q.double(), k.double(), v.double()), 2e-5, 2e-5, "out")
+
+
 @pytest.mark.parametrize("seq", [1, 2, 33, 64, 65, 200, 513])
 @pytest.mark.parametrize("heads", [1, 4])
 def test_backward_matches_oracle(cuda, seq, heads):

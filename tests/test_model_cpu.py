@@ -31,6 +31,18 @@ def test_registry_names_match_the_reference():
         ModelConfig(attention="dilution")
 
 
+def test_mixed_stack_builds():
+    """Layers of different attention types in one stack (reference tests/test_selective_model.py:
+    36-40; its "dilution" layer is not part of this package)."""
+    model = _tiny(layers=3, layer_attention=["selective", "softmax", "selective_x16"])
+    assert [type(b.attn).__name__ for b in model.transformer.h] == [
+        "SelectiveAttention", "CausalSelfAttention", "SelectiveAttention"]
+    assert model.transformer.h[2].attn.exempt == 16
+    idx = torch.randint(0, 97, (2, 40))
+    logits, loss = model(idx, idx)
+    assert logits.shape == (2, 40, 97) and torch.isfinite(loss)
+
+
 def test_parameter_counts():
     """208,540,416 is the reference run record's count for its 16K model
     (runs/scale_16384/all_selective_nope_bos_seed1337/metrics.jsonl:1); d1024/16H is BASELINE's
