@@ -50,6 +50,10 @@ KERNEL_FLOP = {"forward": 2.0 * UNIT, "backward_kv": 4.0 * UNIT, "backward_dq": 
 MEASURED_TRAFFIC_BYTES = {"forward": (2.0 * 530_879 + 67_584) * 1024,
                           "backward_kv": (2.0 * 582_772 + 576_429) * 1024,
                           "backward_dq": (2.0 * 541_704 + 96_256) * 1024}
+# C4 (131072-token prefill, 8 chunks): the forward kernel's HBM bytes per launch (mean over the
+# chunks, FETCH_SIZE x 2.0 + WRITE_SIZE x 1.0) and MFMA busy fraction, measured with rocprofv3:
+# profiles/c4_prefill_kernels.md. The run's own per-launch time turns the bytes into a rate.
+MEASURED_C4 = {"hbm_bytes_per_launch": (2.0 * 1_315_000 + 67_590) * 1024, "mfma_busy": 0.28}
 
 
 def _cpu_model() -> str:
@@ -228,7 +232,14 @@ def main() -> int:
             _progress(f"C3 {geometry} {tr['tokens_per_s']:.0f} tok/s")
         record["train_tok_s"] = round(record["train"]["d768"]["tokens_per_s"], 1)
     if not args.no_configs:
-        record["c4"] = _rounded(harness.prefill_rate(reps=2, warmup=1))
+        c4 = harness.prefill_rate(reps=2, warmup=1)
+        c4["counters"] = {"source": "profiles/c4_prefill_kernels.md (rocprofv3 --pmc)",
+                          "mfma_busy": MEASURED_C4["mfma_busy"],
+                          "hbm_bytes_per_launch": MEASURED_C4["hbm_bytes_per_launch"],
+                          "hbm_tb_s": MEASURED_C4["hbm_bytes_per_launch"] / (c4["per_layer_chunk_forward_ms"] * 1e9),
+                          "hbm_frac_of_peak": MEASURED_C4["hbm_bytes_per_launch"]
+                          / (c4["per_layer_chunk_forward_ms"] * 1e-3) / 8e12}
+        record["c4"] = _rounded(c4)
         torch.cuda.empty_cache()
         _progress(f"C4 {record['c4']['tokens_per_s']:.0f} tok/s")
         record["c5"] = _rounded(harness.perhead_rate(steps=5, warmup=2))
