@@ -98,11 +98,16 @@ def train_step_rate(geometry: str = "d768", steps: int = 10, warmup: int = 3, se
     final = float(losses[-1])
     if not math.isfinite(final):
         raise RuntimeError(f"non-finite training loss {final}")
+    # the attention kernels' share of a step, from their own HIP events over one more step
+    per_step = kernel_times(step, 1, per_call=True)
+    attn_ms = sum(per_step.values())
     tokens = batch * seq
     flop = model_flop_per_token(cfg, seq) * tokens
     return {"config": f"C3 train step, {geometry} ({model.num_parameters()} params), {layers} layers, "
                       f"{batch}x{seq} tokens, bf16 autocast, fused AdamW, eager",
             "tokens_per_s": tokens / (ms * 1e-3), "ms_per_step": ms, "model_tflops": flop / (ms * 1e-3) / 1e12,
+            "attention_kernel_ms": attn_ms, "attention_share": attn_ms / ms,
+            "per_layer_attention_ms": {name: t / layers for name, t in per_step.items()},
             "loss": final, "peak_mem_gib": torch.cuda.max_memory_allocated() / 2**30, "steps": steps,
             "warmup": warmup}
 
