@@ -14,7 +14,11 @@ int launch_bwd_kv_bf16(int D, int G, bool cv, const KvLaunch& a) {
     if (G == 2) { SA_KV(32, 2); }
     SA_KV(32, 1);
   }
-  if (D == 64) { SA_KV(64, 1); }
+  if (D == 64) {   // one head per wavefront at head dim 64: the pipelined kernel
+    if (cv) launch_kv64_from<true>(a);
+    else launch_kv64_from<false>(a);
+    return launch_status();
+  }
   SA_KV(128, 1);
 #undef SA_KV
 }

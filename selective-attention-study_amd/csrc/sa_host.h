@@ -115,8 +115,8 @@ inline BwdLayout bwd_layout(int64_t nseq, int64_t heads, int64_t t, int64_t D, i
   L.qt = take(R * D * ldt * esize);
   L.dot = take(R * D * ldt * esize);
   L.kt = take(R * D * ldt * esize);
-  L.lse = take(R * t * 4);
-  L.dbar = take(R * t * 4);
+  L.lse = take(R * ldt * 4);    // (R, ldt): rows padded per head
+  L.dbar = take(R * ldt * 4);   // -dbar, likewise
   L.dq = take(nseq * t * D * 4);   // head 0's own fp32 sums (the other heads write their views)
   L.dk = take(nseq * t * D * 4);
   L.dq0x = take(nseq * t * D * 4);

@@ -351,6 +351,53 @@ __device__ __forceinline__ BlockXY xcd_block() {
 // (measured: a rotation by r or an XOR by r mod 8 takes twice the cycles).
 __device__ __forceinline__ int swz64(int r, int c) { return r * 64 + (((c + (r >> 1)) & 7) << 3); }
 
+// Unpadded LDS rows of 32 bf16 (four 16-byte chunks), chunk c of row r stored at chunk
+// c ^ ((r / 4) mod 4): a 16-byte read of one chunk by 16 consecutive rows (16 lanes per pass over
+// 64 four-byte banks) touches 16 distinct bank groups.
+__device__ __forceinline__ int swz32(int r, int c) { return r * 32 + ((c ^ ((r >> 2) & 3)) << 3); }
+
+typedef __attribute__((address_space(3))) void* lds_void_ptr;
+
+// A buffer resource over `bytes` bytes from p (loads past them read zero).
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t rsrc(const void* p, int64_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), 0, (int)bytes, RSRC_WORD3);
+}
+
+// Direct loads into LDS: one instruction fills 64 consecutive 16-byte slots (1 KB) from the given
+// LDS base, lane l slot l (measured lane layout on gfx950); each lane reads the global chunk that
+// belongs in its slot, through a buffer resource (the scalar offset counts in the range check,
+// measured: rows past the resource load zero). A [32][64] or [64][32] bf16 tile takes four such
+// loads, parts m = 0..3.
+//   rows64: a [32 rows][64] tile in swz64 layout from rows row0.. of a row-major matrix (row stride
+//           ld elements). Slot 64m + l holds row 8m + l/8, stored chunk l mod 8, so logical chunk
+//           (l mod 8 - l/16 - 4m) mod 8: c0 = (l mod 8 - l/16) mod 8 for even m, c0 ^ 4 for odd m.
+//   cols32: a [64 rows][32] tile in swz32 layout, columns col0.. of one of this library's transposed
+//           copies (row stride ld, zero-filled past T). Slot 64m + l holds row 16m + l/4, logical
+//           chunk (l mod 4) ^ (l/16 mod 4).
+struct RowsLane {
+  int v0, v1;   // the lane's byte offsets for the even and the odd parts
+  __device__ __forceinline__ RowsLane(int ld, int lane) {
+    const int c0 = ((lane & 7) - (lane >> 4)) & 7;
+    v0 = ((lane >> 3) * ld + 8 * c0) * 2;
+    v1 = ((lane >> 3) * ld + 8 * (c0 ^ 4)) * 2;
+  }
+};
+__device__ __forceinline__ int cols_lane(int64_t ld, int lane) {
+  return (int)((lane >> 2) * ld + 8 * ((lane & 3) ^ ((lane >> 4) & 3))) * 2;
+}
+__device__ __forceinline__ void g2l_rows64(uint16_t* tile, __amdgpu_buffer_rsrc_t rs, const RowsLane& rl, int ld,
+                                           int row0, int m) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_void_ptr)(tile + 512 * m), 16, (m & 1) ? rl.v1 : rl.v0,
+                                           (row0 + 8 * m) * ld * 2, 0, 0);
+}
+__device__ __forceinline__ void g2l_cols32(uint16_t* tile, __amdgpu_buffer_rsrc_t rs, int vl, int ld, int col0,
+                                           int m) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_void_ptr)(tile + 512 * m), 16, vl, (16 * m * ld + col0) * 2, 0,
+                                           0);
+}
+// the wavefront's outstanding vector-memory operations (the direct loads included) have completed
+__device__ __forceinline__ void wait_loads() { __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
+
 // Register-staged tiles for software pipelining: load() issues a tile's global loads into registers
 // (each thread owns PER 16-byte chunks), store() later writes them to LDS, so the loads of the next
 // tile are in flight while the current one is computed.
@@ -916,15 +963,17 @@ __global__ __launch_bounds__(NTHREADS, (fwd_min_blocks<OP, D, G>())) void fwd_ke
 }
 
 // ---------------------------------------------------------------------------------------------
-// Backward preparation: lse = rmax + log2(rden), dbar = rowsum(dO * O), and the transposed
-// copies Q^T, dO^T, K^T (R, D, ldt). The statistics take D/8 lanes per row (8 elements each, so
-// the loads of a row are contiguous across its lanes); transposes go by tiles.
+// Backward preparation: lse = rmax + log2(rden), ndbar = -rowsum(dO * O) (negated: the dO.v
+// products accumulate onto it), and the transposed copies Q^T, dO^T, K^T (R, D, ldt). The
+// statistics are laid out (R, ldt), each head's rows padded to ldt with lse = +inf (P = 0) and
+// ndbar = 0, so a 32-row tile of them is always in bounds; they take D/8 lanes per row (8 elements
+// each, so the loads of a row are contiguous across its lanes); transposes go by tiles.
 
 template <class OP, int D>
 __global__ __launch_bounds__(NTHREADS) void bwd_rowstats_kernel(
     const typename OP::elem* __restrict__ dout, Strides dos, int H, int T, const float* __restrict__ out,
     const float* __restrict__ rmax, const float* __restrict__ rden,
-    float* __restrict__ lse, float* __restrict__ dbar, int64_t rows, float4* __restrict__ zero0,
+    float* __restrict__ lse, float* __restrict__ ndbar, int64_t ldt, int64_t rows, float4* __restrict__ zero0,
     float4* __restrict__ zero1, int64_t zero_n4) {
   using elem = typename OP::elem;
   constexpr int LPR = D / 8;   // lanes per row
@@ -934,12 +983,14 @@ __global__ __launch_bounds__(NTHREADS) void bwd_rowstats_kernel(
     zero0[i] = make_float4(0.f, 0.f, 0.f, 0.f);
     zero1[i] = make_float4(0.f, 0.f, 0.f, 0.f);
   }
-  const int64_t r = g / LPR;
+  const int64_t pr = g / LPR;   // padded row: head pr / ldt, row t
   const int part = (int)(g % LPR);
+  const int64_t hr = pr / ldt;   // b * H + head
+  const int t = (int)(pr - hr * ldt);
+  const int64_t r = hr * T + t;
   float acc = 0.f;
-  if (r < rows) {
-    const int64_t hr = r / T;   // b * H + head
-    const elem* dr = dout + dos.at(hr / H, hr % H) + (r - hr * T) * dos.row + part * 8;
+  if (pr < rows && t < T) {
+    const elem* dr = dout + dos.at(hr / H, hr % H) + (int64_t)t * dos.row + part * 8;
     const float* orow = out + r * D + part * 8;
     const float4 o0 = *reinterpret_cast<const float4*>(orow);
     const float4 o1 = *reinterpret_cast<const float4*>(orow + 4);
@@ -956,9 +1007,9 @@ __global__ __launch_bounds__(NTHREADS) void bwd_rowstats_kernel(
   }
 #pragma unroll
   for (int o = LPR / 2; o > 0; o >>= 1) acc += __shfl_xor(acc, o);
-  if (r < rows && part == 0) {
-    dbar[r] = acc;
-    lse[r] = rmax[r] + __log2f(rden[r]);
+  if (pr < rows && part == 0) {
+    ndbar[pr] = t < T ? -acc : 0.f;
+    lse[pr] = t < T ? rmax[r] + __log2f(rden[r]) : INFINITY;
   }
 }
 
@@ -998,7 +1049,10 @@ __global__ __launch_bounds__(NTHREADS) void transpose_kernel(const E* __restrict
 // eight 16-byte row loads (t past T read as zero), the block transposed in registers (each output
 // word joins the same half-word of two rows), eight 16-byte column stores. A wavefront's loads and
 // stores cover whole 128-byte segments (eight lanes per row or column).
-template <int D>
+// CROW: each output row holds its 16-column blocks in C-layout row order (groups of four columns
+// 0, 2, 1, 3), the order in which a transposed operand tile enters the products of the key-side
+// backward kernel at head dim 64, so that its direct loads into LDS are plain copies.
+template <int D, bool CROW>
 __global__ __launch_bounds__(NTHREADS) void transpose8_kernel(const uint16_t* __restrict__ in,
                                                               uint16_t* __restrict__ outT, int T, int64_t ldt,
                                                               Strides is, int H) {
@@ -1024,19 +1078,33 @@ __global__ __launch_bounds__(NTHREADS) void transpose8_kernel(const uint16_t* __
       const uint32_t lo = word(2 * w, e >> 1), hi = word(2 * w + 1, e >> 1);
       o[w] = (e & 1) ? ((lo >> 16) | (hi & 0xFFFF0000u)) : ((lo & 0xFFFFu) | (hi << 16));
     }
-    *reinterpret_cast<uint4*>(dst + (int64_t)(8 * c + e) * ldt) = make_uint4(o[0], o[1], o[2], o[3]);
+    uint16_t* row = dst + (int64_t)(8 * c + e) * ldt;
+    if constexpr (CROW) {
+      // t0 % 16 is 0 or 8: its groups of four a = (t0 % 16) / 4 and a + 1 go to 2 (a mod 2) + a / 2
+      const int a = (int)(t0 & 15) >> 2;
+      uint16_t* blk = row - (t0 & 15);
+      *reinterpret_cast<uint2*>(blk + 4 * (((a & 1) << 1) | (a >> 1))) = make_uint2(o[0], o[1]);
+      *reinterpret_cast<uint2*>(blk + 4 * ((((a + 1) & 1) << 1) | ((a + 1) >> 1))) = make_uint2(o[2], o[3]);
+    } else {
+      *reinterpret_cast<uint4*>(row) = make_uint4(o[0], o[1], o[2], o[3]);
+    }
   }
 }
 
-// in (R views, Strides is) -> outT (R, D, ldt), ldt a multiple of 64, zero past T.
+// in (R views, Strides is) -> outT (R, D, ldt), ldt a multiple of 64, zero past T; crow (2-byte
+// elements): columns in C-layout row order within each 16-column block (transpose8_kernel).
 template <typename E, int D>
 void launch_transpose(const E* in, E* outT, int T, int64_t ldt, const Strides& is, int H, int64_t R,
-                      hipStream_t st) {
+                      hipStream_t st, bool crow = false) {
   if constexpr (sizeof(E) == 2) {
     constexpr int rows_per_block = NTHREADS / (D / 8) * 8;
-    hipLaunchKernelGGL((transpose8_kernel<D>), dim3((unsigned)cdiv(ldt, rows_per_block), (unsigned)R),
-                       dim3(NTHREADS), 0, st, reinterpret_cast<const uint16_t*>(in),
-                       reinterpret_cast<uint16_t*>(outT), T, ldt, is, H);
+    const dim3 grid((unsigned)cdiv(ldt, rows_per_block), (unsigned)R);
+    if (crow)
+      hipLaunchKernelGGL((transpose8_kernel<D, true>), grid, dim3(NTHREADS), 0, st,
+                         reinterpret_cast<const uint16_t*>(in), reinterpret_cast<uint16_t*>(outT), T, ldt, is, H);
+    else
+      hipLaunchKernelGGL((transpose8_kernel<D, false>), grid, dim3(NTHREADS), 0, st,
+                         reinterpret_cast<const uint16_t*>(in), reinterpret_cast<uint16_t*>(outT), T, ldt, is, H);
   } else {
     hipLaunchKernelGGL((transpose_kernel<E, D>), dim3((unsigned)cdiv(ldt, 64), (unsigned)R), dim3(NTHREADS), 0, st,
                        in, outT, T, ldt, is, H);
@@ -1374,11 +1442,9 @@ __global__ __launch_bounds__(NTHREADS, (kv_min_blocks<OP, D, G>())) void bwd_kv_
       nQt[g].load(qt + row * D * ldt, ldt, qbase, tid);
       ndO[g].load(do_rows[g], do_ld, qbase, T, tid);
       ndOt[g].load(dot + row * D * ldt, ldt, qbase, tid);
-      const int r = qbase + (tid & (TILE - 1));
-      const int rr = min(r, T - 1);
-      const float lv = lse[row * T + rr], dv_ = dbar[row * T + rr];
-      nLse[g] = r < T ? lv : INFINITY;   // rows past the end: P = 0
-      nDb[g] = r < T ? -dv_ : 0.f;   // negated: the dO.v product accumulates onto it
+      const int r = qbase + (tid & (TILE - 1));   // < ldt: padded rows hold lse = +inf, -dbar = 0
+      nLse[g] = lse[row * ldt + r];
+      nDb[g] = dbar[row * ldt + r];
     }
     if (!has_h0) {
       nQ[G].load(q_rows[G], q_ld, qbase, T, tid);
@@ -1545,6 +1611,268 @@ __global__ __launch_bounds__(NTHREADS, (kv_min_blocks<OP, D, G>())) void bwd_kv_
 }
 
 // ---------------------------------------------------------------------------------------------
+// Backward, key side, bf16 storage at head dim 64 with one head per wavefront (the instance of
+// C2, C3, C4's model and C5): bwd_kv_kernel's tile work, with every query tile's operands loaded
+// straight from global memory into LDS one tile ahead -- no staging registers, no load latency at
+// the start of a tile, one barrier per tile -- into two buffers of unpadded, swizzled tiles: the Q
+// and dO rows (and head 0's Q rows) in swz64 layout, their transposed copies (which the transpose
+// writes in C-layout column order) in swz32 layout. The wavefront's own K rows sit in registers
+// beside head 0's, its V rows in LDS.
+
+// One tile buffer of bwd_kv64_kernel: the Q, dO, head 0's Q rows (swz64), their transposed copies
+// (swz32), the rows' lse and -dbar (slots 32.. repeat rows 0..31), and per wavefront each lane's
+// carry at the tile's first query.
+struct KvTileBuf64 {
+  __attribute__((aligned(16))) uint16_t r[3][TILE * 64];
+  __attribute__((aligned(16))) uint16_t t[3][TILE * 64];
+  __attribute__((aligned(16))) float stat[2][64];
+  __attribute__((aligned(16))) float hist[NWAVES][64];
+};
+
+template <bool CV>   // CV: every view is the contiguous (nseq, H, T, D) layout of sa_backward
+__global__ __launch_bounds__(NTHREADS, 2) void bwd_kv64_kernel(
+    const uint16_t* __restrict__ q, const uint16_t* __restrict__ k, const uint16_t* __restrict__ v,
+    const uint16_t* __restrict__ qt, const uint16_t* __restrict__ dout, const uint16_t* __restrict__ dot, Strides qs,
+    Strides ks, Strides vs, Strides dos, const float* __restrict__ lse, const float* __restrict__ dbar,
+    const float* __restrict__ carry, float* __restrict__ ucheck, float* __restrict__ dk0h, float* __restrict__ dk0x,
+    GradView dkv, GradView dvv, int nseq, int H, int T, int64_t ldt, int exempt, float scale) {
+  using OP = OpBF16;
+  using elem = uint16_t;
+  using frag = OP::frag;
+  constexpr int D = 64, NS = 4, DB = 2, AS = 2;
+  constexpr int TW = TILE * D;   // elements of a [32][64] tile
+  // The two tile buffers are separate LDS variables, and the tile loop runs in pairs so that
+  // every access names its buffer at compile time: the compiler then knows the direct loads into
+  // one buffer do not write what the tile reads from the other, and waits for them only at the end
+  // of the tile (a single array indexed by tile parity made it wait before the tile's first read).
+  __shared__ KvTileBuf64 sB0, sB1;
+  __shared__ __attribute__((aligned(16))) elem sV[NWAVES][TW];
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = wave_id();
+  const int n = lane & 31, h = lane >> 5;
+  const BlockXY bxy = xcd_block();
+  const int b = bxy.y / H, hh = bxy.y % H;
+  const bool has_h0 = (hh == 0);
+  const int NB = (T + TILE - 1) / TILE;
+  const int key0 = bxy.x * (NWAVES * TILE) + wave * TILE;
+  const int j = key0 + n;
+  const int64_t seq_row = (int64_t)b * H;
+  auto view_head = [&](const elem* base, const Strides& s_, int hd) -> const elem* {
+    if constexpr (CV) return base + (seq_row + hd) * T * D;
+    else return base + s_.at(b, hd);
+  };
+  auto view_ld = [&](const Strides& s_) -> int {
+    if constexpr (CV) return D;
+    else return (int)s_.row;
+  };
+  float* uplane = ucheck + ((int64_t)hh * nseq + b) * utri_floats(NB);
+  const float* carry_b = carry + (int64_t)b * NB * T;
+
+  // B operands (lane = key): the wavefront's K rows and head 0's in registers, its V rows in LDS
+  frag kf[NS], k0f[NS];
+  {
+    const elem* kh = view_head(k, ks, hh);
+    const elem* k0 = view_head(k, ks, 0);
+#pragma unroll
+    for (int s = 0; s < NS; ++s) {
+      kf[s] = ld_std_bounded<OP>(kh, view_ld(ks), j, T, h, s);
+      k0f[s] = has_h0 ? kf[s] : ld_std_bounded<OP>(k0, view_ld(ks), j, T, h, s);
+    }
+    const elem* vh = view_head(v, vs, hh);
+    for (int c = lane; c < TILE * (D / 8); c += 64) {
+      const int r = c / (D / 8), cc = c % (D / 8);
+      const bool ok = key0 + r < T;
+      const uint4 v4 = *reinterpret_cast<const uint4*>(vh + (int64_t)(ok ? key0 + r : 0) * view_ld(vs) + cc * 8);
+      *reinterpret_cast<uint4*>(&sV[wave][swz64(r, cc)]) = ok ? v4 : make_uint4(0u, 0u, 0u, 0u);
+    }
+  }
+
+  f32x16 dkt[DB], dvt[DB], dk0t[DB];
+#pragma unroll
+  for (int db = 0; db < DB; ++db) {
+    dkt[db] = zero16();
+    dvt[db] = zero16();
+    dk0t[db] = zero16();
+  }
+  float ucarry = 0.f;
+  const float sl2 = scale * LOG2E;
+  const float neg_inv_scale = -1.f / scale;
+  // query tiles the workgroup visits, last to first: NB-1 down to the first that reaches its keys
+  const int qb_lo = bxy.x * NWAVES;
+  const int ntiles = NB - qb_lo;
+
+  // operand sources (buffer resources over one head's rows, or its transposed copy) and this
+  // lane's parts of the direct loads
+  const int q_ld = view_ld(qs), do_ld = view_ld(dos);
+  const __amdgpu_buffer_rsrc_t rs_q = rsrc(view_head(q, qs, hh), (int64_t)T * q_ld * 2);
+  const __amdgpu_buffer_rsrc_t rs_do = rsrc(view_head(dout, dos, hh), (int64_t)T * do_ld * 2);
+  const __amdgpu_buffer_rsrc_t rs_q0 = rsrc(view_head(q, qs, 0), (int64_t)T * q_ld * 2);
+  const __amdgpu_buffer_rsrc_t rs_qt = rsrc(qt + (seq_row + hh) * D * ldt, (int64_t)D * ldt * 2);
+  const __amdgpu_buffer_rsrc_t rs_dot = rsrc(dot + (seq_row + hh) * D * ldt, (int64_t)D * ldt * 2);
+  const __amdgpu_buffer_rsrc_t rs_q0t = rsrc(qt + seq_row * D * ldt, (int64_t)D * ldt * 2);
+  const __amdgpu_buffer_rsrc_t rs_lse = rsrc(lse + (seq_row + hh) * ldt, ldt * 4);
+  const __amdgpu_buffer_rsrc_t rs_ndb = rsrc(dbar + (seq_row + hh) * ldt, ldt * 4);
+  const RowsLane rl_q(q_ld, lane), rl_do(do_ld, lane);
+  const int cl = cols_lane(ldt, lane);
+
+  // Everything query tile qb needs, into buffer B, by direct loads only (the tile loop holds no
+  // register loads: the vector-memory counter drains in issue order, so waiting for one would wait
+  // for the tiles behind it): part `wave` of each operand tile (each wavefront loads a quarter of
+  // every tile), the row statistics (wavefronts 0, 1), and each wavefront's carry row of its keys
+  // (keys past the end read zero).
+  auto load_tile = [&](int qb, KvTileBuf64& B) {
+    const int qbase = qb * TILE;
+    if (wave == 0)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rs_lse, (lds_void_ptr)B.stat[0], 4, (lane & 31) * 4, qbase * 4, 0, 0);
+    if (wave == 1)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rs_ndb, (lds_void_ptr)B.stat[1], 4, (lane & 31) * 4, qbase * 4, 0, 0);
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc(carry_b + (int64_t)qb * T, (int64_t)T * 4),
+                                             (lds_void_ptr)B.hist[wave], 4, j * 4, 0, 0, 0);
+    g2l_rows64(B.r[0], rs_q, rl_q, q_ld, qbase, wave);
+    g2l_rows64(B.r[1], rs_do, rl_do, do_ld, qbase, wave);
+    g2l_cols32(B.t[0], rs_qt, cl, (int)ldt, qbase, wave);
+    g2l_cols32(B.t[1], rs_dot, cl, (int)ldt, qbase, wave);
+    if (!has_h0) {
+      g2l_rows64(B.r[2], rs_q0, rl_q, q_ld, qbase, wave);
+      g2l_cols32(B.t[2], rs_q0t, cl, (int)ldt, qbase, wave);
+    }
+  };
+  // the first tile (NB - 1)
+  load_tile(NB - 1, sB0);
+  wait_loads();
+  __syncthreads();
+
+  // acc[db] (D x keys) += Y^T X: Y a transposed tile (rows d, queries in C-layout order, swz32), X
+  // a C-layout (queries x keys) tile; with split, X also enters as its rounding residual.
+  auto acc_t = [&](f32x16 (&acc)[DB], const elem* yt, const f32x16& x, bool split) {
+    frag xf[AS];
+#pragma unroll
+    for (int s = 0; s < AS; ++s) xf[s] = OP::from_acc(x, s);
+#pragma unroll
+    for (int db = 0; db < DB; ++db)
+#pragma unroll
+      for (int s = 0; s < AS; ++s)
+        acc[db] = OP::mma(*reinterpret_cast<const frag*>(yt + swz32(db * 32 + n, 2 * s + h)), xf[s], acc[db]);
+    if (split) {
+#pragma unroll
+      for (int s = 0; s < AS; ++s) xf[s] = OP::from_acc_lo(x, s);
+#pragma unroll
+      for (int db = 0; db < DB; ++db)
+#pragma unroll
+        for (int s = 0; s < AS; ++s)
+          acc[db] = OP::mma(*reinterpret_cast<const frag*>(yt + swz32(db * 32 + n, 2 * s + h)), xf[s], acc[db]);
+    }
+  };
+  // fragment s of row n of a swz64 tile (A operand: lane = query row; or B: lane = key)
+  auto rfrag = [&](const elem* tile, int s) -> frag {
+    return *reinterpret_cast<const frag*>(tile + swz64(n, 2 * s + h));
+  };
+
+  // Keys below `exempt` are never selected, so they gather attention from every later query and
+  // their dV / dK sums run over all of them: their products take the split operands.
+  const bool split_keys = key0 < exempt;
+
+  // the tile loop in two instances, for head 0's workgroups and the others (see bwd_kv_kernel)
+  auto sweep = [&](auto h0_tag) {
+    constexpr bool H0 = decltype(h0_tag)::value;
+    // tile t (buffer t mod 2, named by ODD)
+    auto tile_step = [&](int t, auto interior_tag, auto odd_tag) {
+      constexpr bool INTERIOR = decltype(interior_tag)::value;
+      constexpr bool ODD = decltype(odd_tag)::value;
+      KvTileBuf64& B = ODD ? sB1 : sB0;
+      const int qb = NB - 1 - t;
+      const int qbase = qb * TILE;
+      const bool more = t + 1 < ntiles;
+      if (more) load_tile(qb - 1, ODD ? sB0 : sB1);   // into the other buffer, free since the last barrier
+      if (INTERIOR || qbase + TILE - 1 >= key0) {   // else every query of the tile precedes every key
+        if (h == 0 && j < T) uplane[utri_row(qb) + j] = ucarry;   // j < (qb + 1) * TILE here
+        const bool edge = !INTERIOR && ((qbase <= key0 + TILE - 1) || key0 < exempt);
+        const bool split = !INTERIOR && split_keys;
+        const TileMasks mk(j, qbase, T, exempt, h);
+        auto body = [&]() {
+          const float hist = B.hist[wave][lane];
+          const elem* q0s = H0 ? B.r[0] : B.r[2];
+          f32x16 l0 = zero16();
+#pragma unroll
+          for (int s = 0; s < NS; ++s) l0 = OP::mma(rfrag(q0s, s), H0 ? kf[s] : k0f[s], l0);
+          f32x16 fs;
+          uint32_t gate;
+          selection_tile<false>(l0, (j < T) ? hist * neg_inv_scale : 0.f, h, edge, mk, gate, fs);
+
+          f32x16 lg;   // q.k - F/s
+          if constexpr (H0) {   // head 0 itself: its logits are l0
+#pragma unroll
+            for (int i = 0; i < 16; ++i) lg[i] = l0[i] + fs[i];
+          } else {
+            lg = fs;
+#pragma unroll
+            for (int s = 0; s < NS; ++s) lg = OP::mma(rfrag(B.r[0], s), kf[s], lg);
+          }
+          f32x16 dp = rows16(B.stat[1], h);   // dO.v - dbar
+#pragma unroll
+          for (int s = 0; s < NS; ++s) dp = OP::mma(rfrag(B.r[1], s), rfrag(sV[wave], s), dp);
+          f32x16 pr, dz;
+          p_dz_tile<false>(lg, dp, B.stat[0], sl2, h, edge, mk, pr, dz);
+          acc_t(dvt, B.t[1], pr, split);
+          f32x16 gp;
+          ucarry = gpath_tile(dz, ucarry, gate, h, gp);
+          if constexpr (H0) {   // head 0's dK takes g with its own dz
+#pragma unroll
+            for (int i = 0; i < 16; ++i) dz[i] += gp[i];
+            acc_t(dkt, B.t[0], dz, true);
+          } else {
+            acc_t(dkt, B.t[0], dz, split);
+            acc_t(dk0t, B.t[2], gp, big_tile(gp));
+          }
+        };
+        body();
+      }
+      wait_loads();
+      __syncthreads();   // the next tile's operands are in; every wavefront is done with this one
+    };
+    // The last NWAVES tiles hold the wavefronts' diagonals; a workgroup with an exempt key runs
+    // every tile with the masks.
+    const int n_int = (qb_lo * TILE < exempt) ? 0 : max(ntiles - NWAVES, 0);
+    // tiles [t0, t1) in pairs, even tiles from buffer 0 and odd ones from buffer 1
+    auto run = [&](int t0, int t1, auto interior_tag) {
+      int t = t0;
+      if (t < t1 && (t & 1)) tile_step(t++, interior_tag, std::true_type{});
+      for (; t + 1 < t1; t += 2) {
+        tile_step(t, interior_tag, std::false_type{});
+        tile_step(t + 1, interior_tag, std::true_type{});
+      }
+      if (t < t1) tile_step(t, interior_tag, std::false_type{});
+    };
+    run(0, n_int, std::true_type{});
+    run(n_int, ntiles, std::false_type{});
+  };
+  if (has_h0) sweep(std::true_type{});
+  else sweep(std::false_type{});
+
+  if (j >= T) return;
+  // dV and the dK of heads other than 0 go to the caller's views; head 0's dK to its fp32 sums,
+  // where the other heads' shares join it
+#pragma unroll
+  for (int db = 0; db < DB; ++db)
+#pragma unroll
+    for (int a = 0; a < 4; ++a) {
+      const int d = db * 32 + 8 * a + 4 * h;
+      const float4 kq = make_float4(dkt[db][4 * a] * scale, dkt[db][4 * a + 1] * scale, dkt[db][4 * a + 2] * scale,
+                                    dkt[db][4 * a + 3] * scale);
+      store_grad4(dvv, b, hh, j, d, make_float4(dvt[db][4 * a], dvt[db][4 * a + 1], dvt[db][4 * a + 2], dvt[db][4 * a + 3]));
+      if (has_h0) *reinterpret_cast<float4*>(dk0h + ((int64_t)b * T + j) * D + d) = kq;
+      else store_grad4(dkv, b, hh, j, d, kq);
+    }
+  if (!has_h0) {
+    float* dst = dk0x + ((int64_t)b * T + j) * D;
+#pragma unroll
+    for (int db = 0; db < DB; ++db)
+#pragma unroll
+      for (int i = 0; i < 16; ++i) atomicAdd(dst + db * 32 + crow(i, h), dk0t[db][i] * scale);
+  }
+}
+
+// ---------------------------------------------------------------------------------------------
 // Backward, query side. grid (ceil(T/128), nseq * H/G); wavefront w owns queries
 // [x*128 + 32w, +32) of heads [gi*G, gi*G+G) (late query blocks launch first) and walks the key
 // tiles up to its diagonal, with Q, dO and the dQ sums in registers. It recomputes P and dz as the
@@ -1628,9 +1956,9 @@ __global__ __launch_bounds__(NTHREADS, (dq_min_blocks<OP, D>())) void bwd_dq_ker
     for (int i = 0; i < 16; ++i) {
       const int r = qbase + crow(i, h);
       const int rr = min(r, T - 1);
-      const float lv = lse[row * T + rr], dv_ = dbar[row * T + rr];
+      const float lv = lse[row * ldt + rr], dv_ = dbar[row * ldt + rr];
       lse_r[g][i] = (r < T) ? lv : INFINITY;   // rows past the end: P = 0
-      ndb_r[g][i] = (r < T) ? -dv_ : 0.f;     // negated: dO.v accumulates onto it
+      ndb_r[g][i] = (r < T) ? dv_ : 0.f;      // -dbar: dO.v accumulates onto it
     }
   }
   if (!has_h0) {
@@ -2254,6 +2582,16 @@ void launch_kv_from(const KvLaunch& a) {
                      a.scale);
 }
 
+template <bool CV>
+void launch_kv64_from(const KvLaunch& a) {
+  dim3 grid((unsigned)cdiv(a.T, NWAVES * TILE), (unsigned)(a.nseq * a.H));
+  hipLaunchKernelGGL((bwd_kv64_kernel<CV>), grid, dim3(NTHREADS), 0, a.st, static_cast<const uint16_t*>(a.q),
+                     static_cast<const uint16_t*>(a.k), static_cast<const uint16_t*>(a.v),
+                     static_cast<const uint16_t*>(a.qt), static_cast<const uint16_t*>(a.dout),
+                     static_cast<const uint16_t*>(a.dot), a.qs, a.ks, a.vs, a.dos, a.lse, a.dbar, a.carry, a.ucheck,
+                     a.dk0h, a.dk0x, a.dkv, a.dvv, a.nseq, a.H, a.T, a.ldt, a.exempt, a.scale);
+}
+
 // The two backward kernels; returns the launch status.
 template <class OP, int D, int G>
 int launch_bwd(const BwdCall& c, const typename OP::elem* qt, const typename OP::elem* kt,
@@ -2327,11 +2665,14 @@ int backward_impl(const BwdCall& c) {
   const elem* k = static_cast<const elem*>(c.k);
   const elem* dout = static_cast<const elem*>(c.dout);
 
-  launch_transpose<elem, D>(q, qt, T, ldt, c.qs, H, R, st);
-  launch_transpose<elem, D>(dout, dot, T, ldt, c.dos, H, R, st);
+  // bf16 at head dim 64: Q^T and dO^T in the column order of the key side's direct loads
+  // (bwd_kv64_kernel)
+  const bool crow = sizeof(elem) == 2 && D == 64;
+  launch_transpose<elem, D>(q, qt, T, ldt, c.qs, H, R, st, crow);
+  launch_transpose<elem, D>(dout, dot, T, ldt, c.dos, H, R, st, crow);
   launch_transpose<elem, D>(k, kt, T, ldt, c.ks, H, R, st);
-  hipLaunchKernelGGL((bwd_rowstats_kernel<OP, D>), dim3((unsigned)cdiv(R * T * (D / 8), NTHREADS)), dim3(NTHREADS),
-                     0, st, dout, c.dos, H, T, c.out, c.rmax, c.rden, lse, dbar, R * T,
+  hipLaunchKernelGGL((bwd_rowstats_kernel<OP, D>), dim3((unsigned)cdiv(R * ldt * (D / 8), NTHREADS)),
+                     dim3(NTHREADS), 0, st, dout, c.dos, H, T, c.out, c.rmax, c.rden, lse, dbar, ldt, R * ldt,
                      // head 0's shares from the other groups are atomic targets (one add per element
                      // and group): cleared here
                      reinterpret_cast<float4*>(dq0x), reinterpret_cast<float4*>(dk0x),
