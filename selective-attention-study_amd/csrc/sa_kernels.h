@@ -2197,6 +2197,252 @@ __global__ __launch_bounds__(NTHREADS, (dq_min_blocks<OP, D>())) void bwd_dq_ker
   }
 }
 
+// ---------------------------------------------------------------------------------------------
+// Backward, query side, bf16 storage at head dim 64 with one head per wavefront: bwd_dq_kernel's
+// tile work with every key tile's operands -- the K, V and head 0's K rows (swz64), K^T and head
+// 0's K^T (swz32), and each wavefront's carry and selection-suffix checkpoint values of the tile's
+// keys -- loaded straight into LDS one tile ahead, two buffers as separate LDS variables (see
+// bwd_kv64_kernel); one barrier per tile.
+
+struct DqTileBuf64 {
+  __attribute__((aligned(16))) uint16_t k[2][TILE * 64];    // K rows, head 0's K rows
+  __attribute__((aligned(16))) uint16_t v[TILE * 64];       // V rows
+  __attribute__((aligned(16))) uint16_t kt[2][TILE * 64];   // K^T, head 0's K^T
+  __attribute__((aligned(16))) float hist[NWAVES][64];      // per wavefront: each lane's key's carry
+  __attribute__((aligned(16))) float uin[NWAVES][64];       // ... and its U checkpoint
+};
+
+template <bool CV>   // CV: every view is the contiguous (nseq, H, T, D) layout of sa_backward
+__global__ __launch_bounds__(NTHREADS, 2) void bwd_dq64_kernel(
+    const uint16_t* __restrict__ q, const uint16_t* __restrict__ k, const uint16_t* __restrict__ v,
+    const uint16_t* __restrict__ kt, const uint16_t* __restrict__ dout, Strides qs, Strides ks, Strides vs,
+    Strides dos, const float* __restrict__ lse, const float* __restrict__ dbar, const float* __restrict__ carry,
+    const float* __restrict__ ucheck, float* __restrict__ dq0h, float* __restrict__ dq0x, GradView dqv, int nseq,
+    int H, int T, int64_t ldt, int exempt, float scale) {
+  using OP = OpBF16;
+  using elem = uint16_t;
+  using frag = OP::frag;
+  constexpr int D = 64, NS = 4, DB = 2, AS = 2;
+  __shared__ DqTileBuf64 sB0, sB1;
+  __shared__ __attribute__((aligned(16))) elem sZ[NWAVES][TILE * TILE];   // per wavefront: dz, g transposed
+  __shared__ __attribute__((aligned(16))) float sRow[NWAVES][2][TILE];   // per wavefront: its rows' lse, -dbar
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = wave_id();
+  const int n = lane & 31, h = lane >> 5;
+  const BlockXY bxy = xcd_block();
+  const int b = bxy.y / H, hh = bxy.y % H;
+  const bool has_h0 = (hh == 0);
+  const int NB = (T + TILE - 1) / TILE;
+  const int qsb = gridDim.x - 1 - bxy.x;
+  const int qb = qsb * NWAVES + wave;
+  const int qbase = qb * TILE;
+  const int64_t seq_row = (int64_t)b * H;
+  auto view_head = [&](const elem* base, const Strides& s_, int hd) -> const elem* {
+    if constexpr (CV) return base + (seq_row + hd) * T * D;
+    else return base + s_.at(b, hd);
+  };
+  auto view_ld = [&](const Strides& s_) -> int {
+    if constexpr (CV) return D;
+    else return (int)s_.row;
+  };
+  const int my_end = (qb < NB) ? qb + 1 : 0;
+  const int wg_end = min(qsb * NWAVES + NWAVES - 1, NB - 1) + 1;
+  elem* zs = sZ[wave];
+  const int qb_c = qb < NB ? qb : NB - 1;
+
+  // A operands (lane = query row): the Q, dO rows and head 0's Q rows in registers; the rows'
+  // statistics in the wavefront's LDS rows (registers would spill)
+  frag qa[NS], doa[NS], q0a[NS];
+#pragma unroll
+  for (int s = 0; s < NS; ++s) {
+    qa[s] = ld_std_bounded<OP>(view_head(q, qs, hh), view_ld(qs), qbase + n, T, h, s);
+    doa[s] = ld_std_bounded<OP>(view_head(dout, dos, hh), view_ld(dos), qbase + n, T, h, s);
+  }
+  if (!has_h0) {
+#pragma unroll
+    for (int s = 0; s < NS; ++s) q0a[s] = ld_std_bounded<OP>(view_head(q, qs, 0), view_ld(qs), qbase + n, T, h, s);
+  }
+  if (lane < TILE) {
+    const int64_t row = seq_row + hh;
+    const int r = qbase + lane;
+    const int rr = min(r, T - 1);
+    const float lv = lse[row * ldt + rr], dv_ = dbar[row * ldt + rr];
+    sRow[wave][0][lane] = (r < T) ? lv : INFINITY;   // rows past the end: P = 0
+    sRow[wave][1][lane] = (r < T) ? dv_ : 0.f;       // -dbar: dO.v accumulates onto it
+  }
+
+  f32x16 dqacc[DB], dq0acc[DB];
+#pragma unroll
+  for (int db = 0; db < DB; ++db) {
+    dqacc[db] = zero16();
+    dq0acc[db] = zero16();
+  }
+  const float sl2 = scale * LOG2E;
+  const float neg_inv_scale = -1.f / scale;
+
+  // key-side sources (buffer resources over one head's rows, or its transposed copy), this
+  // wavefront's rows of the carry and of the U checkpoints (keys past them read zero)
+  const int k_ld = view_ld(ks), v_ld = view_ld(vs);
+  const __amdgpu_buffer_rsrc_t rs_k = rsrc(view_head(k, ks, hh), (int64_t)T * k_ld * 2);
+  const __amdgpu_buffer_rsrc_t rs_k0 = rsrc(view_head(k, ks, 0), (int64_t)T * k_ld * 2);
+  const __amdgpu_buffer_rsrc_t rs_v = rsrc(view_head(v, vs, hh), (int64_t)T * v_ld * 2);
+  const __amdgpu_buffer_rsrc_t rs_kt = rsrc(kt + (seq_row + hh) * D * ldt, (int64_t)D * ldt * 2);
+  const __amdgpu_buffer_rsrc_t rs_k0t = rsrc(kt + seq_row * D * ldt, (int64_t)D * ldt * 2);
+  const __amdgpu_buffer_rsrc_t rs_c = rsrc(carry + ((int64_t)b * NB + qb_c) * T, (int64_t)T * 4);
+  const __amdgpu_buffer_rsrc_t rs_u =
+      rsrc(ucheck + ((int64_t)hh * nseq + b) * utri_floats(NB) + utri_row(qb_c), (int64_t)(qb_c + 1) * TILE * 4);
+  const RowsLane rl_k(k_ld, lane), rl_v(v_ld, lane);
+  const int cl = cols_lane(ldt, lane);
+
+  // everything key tile ktile needs, into buffer B, by direct loads only (see bwd_kv64_kernel)
+  auto load_tile = [&](int ktile, DqTileBuf64& B) {
+    const int kbase = ktile * TILE;
+    g2l_rows64(B.k[0], rs_k, rl_k, k_ld, kbase, wave);
+    g2l_rows64(B.v, rs_v, rl_v, v_ld, kbase, wave);
+    g2l_cols32(B.kt[0], rs_kt, cl, (int)ldt, kbase, wave);
+    if (!has_h0) {
+      g2l_rows64(B.k[1], rs_k0, rl_k, k_ld, kbase, wave);
+      g2l_cols32(B.kt[1], rs_k0t, cl, (int)ldt, kbase, wave);
+    }
+    const int jo = (kbase + n) * 4;
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(rs_c, (lds_void_ptr)B.hist[wave], 4, jo, 0, 0, 0);
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(rs_u, (lds_void_ptr)B.uin[wave], 4, jo, 0, 0, 0);
+  };
+  // fragment s of row n (lane = key) of a swz64 tile
+  auto rfrag = [&](const elem* tile, int s) -> frag {
+    return *reinterpret_cast<const frag*>(tile + swz64(n, 2 * s + h));
+  };
+  // acc[db] (queries x D) += X K: X a C-layout (queries x keys) tile sent through the wavefront's
+  // LDS tile to become the A operand (transposed write, transposing read), K^T (swz32) the B
+  // operand; with split, X's rounding residual takes a second pass.
+  auto acc_xk = [&](f32x16 (&acc)[DB], const f32x16& x, const elem* ktile, bool split) {
+    frag zf[AS];
+    put_tr<false>(zs, x, n, h);
+    lds_wave_sync();
+#pragma unroll
+    for (int s = 0; s < AS; ++s) zf[s] = get_tr(zs, lane, s);
+#pragma unroll
+    for (int db = 0; db < DB; ++db)
+#pragma unroll
+      for (int s = 0; s < AS; ++s)
+        acc[db] = OP::mma(zf[s], *reinterpret_cast<const frag*>(ktile + swz32(db * 32 + n, 2 * s + h)), acc[db]);
+    if (split) {
+      lds_wave_sync();
+      put_tr<true>(zs, x, n, h);
+      lds_wave_sync();
+#pragma unroll
+      for (int s = 0; s < AS; ++s) zf[s] = get_tr(zs, lane, s);
+#pragma unroll
+      for (int db = 0; db < DB; ++db)
+#pragma unroll
+        for (int s = 0; s < AS; ++s)
+          acc[db] = OP::mma(zf[s], *reinterpret_cast<const frag*>(ktile + swz32(db * 32 + n, 2 * s + h)), acc[db]);
+    }
+    lds_wave_sync();
+  };
+
+  // the first key tile
+  load_tile(0, sB0);
+  wait_loads();
+  __syncthreads();
+
+  // the tile loop in two instances, for head 0's workgroups and the others (see bwd_kv_kernel)
+  auto sweep = [&](auto h0_tag) {
+    constexpr bool H0 = decltype(h0_tag)::value;
+    // key tile ktile (buffer ktile mod 2, named by ODD); INTERIOR: no pair of the tile is masked or
+    // exempt for any wavefront
+    auto tile_step = [&](int ktile, auto interior_tag, auto odd_tag) {
+      constexpr bool INTERIOR = decltype(interior_tag)::value;
+      constexpr bool ODD = decltype(odd_tag)::value;
+      DqTileBuf64& B = ODD ? sB1 : sB0;
+      const int kbase = ktile * TILE;
+      if (ktile + 1 < wg_end) load_tile(ktile + 1, ODD ? sB0 : sB1);   // free since the last barrier
+      if (ktile < my_end) {
+        const int j = kbase + n;
+        const bool edge = !INTERIOR && ((kbase + TILE - 1 >= qbase) || (kbase + TILE > T) || kbase < exempt);
+        const TileMasks mk(j, qbase, T, exempt, h);
+        const float hist = B.hist[wave][lane], uin = B.uin[wave][lane];
+        const elem* k0s = H0 ? B.k[0] : B.k[1];
+        f32x16 l0 = zero16();
+#pragma unroll
+        for (int s = 0; s < NS; ++s) l0 = OP::mma(H0 ? qa[s] : q0a[s], rfrag(k0s, s), l0);
+        f32x16 fs;
+        uint32_t gate;
+        selection_tile<false>(l0, hist * neg_inv_scale, h, edge, mk, gate, fs);
+        f32x16 lg;   // q.k - F/s
+        if constexpr (H0) {   // head 0 itself: its logits are l0
+#pragma unroll
+          for (int i = 0; i < 16; ++i) lg[i] = l0[i] + fs[i];
+        } else {
+          lg = fs;
+#pragma unroll
+          for (int s = 0; s < NS; ++s) lg = OP::mma(qa[s], rfrag(B.k[0], s), lg);
+        }
+        f32x16 dp = rows16(sRow[wave][1], h);   // dO.v - dbar
+#pragma unroll
+        for (int s = 0; s < NS; ++s) dp = OP::mma(doa[s], rfrag(B.v, s), dp);
+        f32x16 pr, dz;
+        p_dz_tile<false>(lg, dp, sRow[wave][0], sl2, h, edge, mk, pr, dz);
+        f32x16 gp;
+        gpath_tile(dz, uin, gate, h, gp);
+        if constexpr (H0) {   // head 0's dQ takes g with its own dz
+#pragma unroll
+          for (int i = 0; i < 16; ++i) dz[i] += gp[i];
+          acc_xk(dqacc, dz, B.kt[0], true);
+        } else {
+          acc_xk(dqacc, dz, B.kt[0], false);
+          acc_xk(dq0acc, gp, B.kt[1], big_tile(gp));
+        }
+      }
+      wait_loads();
+      __syncthreads();   // the next tile's operands are in; every wavefront is done with this one
+    };
+    auto run = [&](int t0, int t1, auto interior_tag) {
+      int t = t0;
+      if (t < t1 && (t & 1)) tile_step(t++, interior_tag, std::true_type{});
+      for (; t + 1 < t1; t += 2) {
+        tile_step(t, interior_tag, std::false_type{});
+        tile_step(t + 1, interior_tag, std::true_type{});
+      }
+      if (t < t1) tile_step(t, interior_tag, std::false_type{});
+    };
+    // tiles holding exempt keys, then the interior ones (below every wavefront's diagonal, which
+    // also keeps them clear of the sequence end), then the diagonals
+    const int i_lo = min((exempt + TILE - 1) / TILE, wg_end);
+    const int i_hi = max(i_lo, min(qsb * NWAVES, wg_end));
+    run(0, i_lo, std::false_type{});
+    run(i_lo, i_hi, std::true_type{});
+    run(i_hi, wg_end, std::false_type{});
+  };
+  if (has_h0) sweep(std::true_type{});
+  else sweep(std::false_type{});
+
+  if (qb >= NB) return;
+  // heads other than 0: dQ (scaled) to the caller's view; head 0: unscaled fp32 sums, where the
+  // other heads' shares join it
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    const int r = qbase + crow(i, h);
+    if (r < T) {
+#pragma unroll
+      for (int db = 0; db < DB; ++db) {
+        if (has_h0) dq0h[((int64_t)b * T + r) * D + db * 32 + n] = dqacc[db][i];
+        else store_grad1(dqv, b, hh, r, db * 32 + n, dqacc[db][i] * scale);
+      }
+    }
+  }
+  if (!has_h0) {
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      const int r = qbase + crow(i, h);
+      if (r < T) {
+#pragma unroll
+        for (int db = 0; db < DB; ++db) atomicAdd(dq0x + ((int64_t)b * T + r) * D + db * 32 + n, dq0acc[db][i]);
+      }
+    }
+  }
+}
+
 // Gradients to the output dtype (bf16 or fp32): dq*scale, dk, dv, with head 0's dQ and dK shares
 // from the other head groups (dq0x unscaled, dk0x scaled) added to head 0.
 
@@ -2634,8 +2880,17 @@ int launch_bwd(const BwdCall& c, const typename OP::elem* qt, const typename OP:
   }
   {
     TimedLaunch timed(SA_KERNEL_BACKWARD_DQ, c.st);
-    if (cv) SA_LAUNCH_DQ(true);
-    else SA_LAUNCH_DQ(false);
+    if constexpr (sizeof(elem) == 2 && D == 64 && G == 1) {   // one head per wavefront: the pipelined kernel
+#define SA_LAUNCH_DQ64(CVV)                                                                                        \
+  hipLaunchKernelGGL((bwd_dq64_kernel<CVV>), grid, dim3(NTHREADS), 0, c.st, q, k, v, kt, dout, c.qs, c.ks, c.vs,    \
+                     c.dos, lse, dbar, c.carry, ucheck, dq0h, dq0x, dqv, c.nseq, c.H, c.T, ldt, c.exempt, c.scale)
+      if (cv) SA_LAUNCH_DQ64(true);
+      else SA_LAUNCH_DQ64(false);
+#undef SA_LAUNCH_DQ64
+    } else {
+      if (cv) SA_LAUNCH_DQ(true);
+      else SA_LAUNCH_DQ(false);
+    }
   }
 #undef SA_LAUNCH_DQ
   return launch_status();
