@@ -763,19 +763,23 @@ __global__ __launch_bounds__(NTHREADS, (fwd_min_blocks<OP, D, G>())) void fwd_ke
   k_rows[G] = k_head(0);
   const int k_ldi = (int)k_ld;
   float nC = 0.f;
+  bool nC_ok = false;
+  // (every load is unconditional and the loaded values are first used when stored: the vector-
+  // memory counter drains in issue order, so a wait inside the tile for one of them, or at a join
+  // after a conditional one, would wait for the whole next tile)
   auto load_tile = [&](int kt) {
     const int kbase = kt * TILE;
+    const int w = (tid >> 5) & (NWAVES - 1);
+    const int rbw = min(qsb * NWAVES + w, NBq - 1);
+    const int jj = kbase + (tid & (TILE - 1));
+    nC = carry[((int64_t)b * NBq + rbw) * Tk + min(jj, Tk - 1)];   // scaled (zero past the end) when stored
+    nC_ok = jj < Tk;
 #pragma unroll
     for (int g = 0; g < G; ++g) {
       nK[g].load(k_rows[g], k_ldi, kbase, Tk, tid);
       nVt[g].load(vt + (seq_row + hd0 + g) * D * ldv, ldv, kbase, tid);
     }
-    if (!has_h0) nK[G].load(k_rows[G], k_ldi, kbase, Tk, tid);
-    const int w = (tid >> 5) & (NWAVES - 1);
-    const int rbw = min(qsb * NWAVES + w, NBq - 1);
-    const int jj = kbase + (tid & (TILE - 1));
-    const float c = carry[((int64_t)b * NBq + rbw) * Tk + min(jj, Tk - 1)];
-    nC = (jj < Tk) ? c * neg_inv_scale : 0.f;
+    nK[G].load(k_rows[G], k_ldi, kbase, Tk, tid);   // head 0's rows (its own group's copy unused)
   };
   auto store_tile = [&](int buf) {
 #pragma unroll
@@ -784,7 +788,7 @@ __global__ __launch_bounds__(NTHREADS, (fwd_min_blocks<OP, D, G>())) void fwd_ke
       nVt[g].template store_crow<LDV>(sVt[buf][g], tid);
     }
     if (!has_h0) nK[G].template store<LDK>(sK[buf][G], tid);
-    if (tid < NWAVES * TILE) sC[buf][tid >> 5][tid & (TILE - 1)] = nC;
+    if (tid < NWAVES * TILE) sC[buf][tid >> 5][tid & (TILE - 1)] = nC_ok ? nC * neg_inv_scale : 0.f;
   };
 
   // the next key tile is loaded into registers while this one is computed (stored to the other LDS
