@@ -967,6 +967,284 @@ __global__ __launch_bounds__(NTHREADS, (fwd_min_blocks<OP, D, G>())) void fwd_ke
 }
 
 // ---------------------------------------------------------------------------------------------
+// Forward, bf16 storage at head dim 64 with two heads per wavefront (the default there): fwd_kernel's
+// tile work with every key tile's operands -- the K rows of both heads and head 0's (swz64), their
+// V^T (swz32, written in C-layout column order by the transpose), and each wavefront's carry row
+// -- loaded straight into LDS one tile ahead, two buffers as separate LDS variables and the tile
+// loop run in pairs (see bwd_kv64_kernel); one barrier per tile.
+
+struct FwdTileBuf64 {
+  __attribute__((aligned(16))) uint16_t k[3][TILE * 64];    // K rows of the two heads, head 0's
+  __attribute__((aligned(16))) uint16_t vt[2][TILE * 64];   // V^T of the two heads
+  __attribute__((aligned(16))) float c[NWAVES][64];         // per wavefront: the carry of each key
+};
+
+template <bool CV>   // CV: as fwd_kernel
+__global__ __launch_bounds__(NTHREADS, 2) void fwd64_kernel(
+    const uint16_t* __restrict__ q, const uint16_t* __restrict__ k, const uint16_t* __restrict__ vt,
+    const float* __restrict__ carry, float* __restrict__ out, float* __restrict__ rmax, float* __restrict__ rden,
+    uint16_t* __restrict__ y, Strides ys, int H, int Tq, int Tk, Strides qs, Strides ks, int q_off, int64_t ldv,
+    int exempt, float scale, int damp_mode, float train_len) {
+  using OP = OpBF16;
+  using elem = uint16_t;
+  using frag = OP::frag;
+  constexpr int D = 64, G = 2, NS = 4, DB = 2, AS = 2;
+  __shared__ FwdTileBuf64 sB0, sB1;
+  constexpr int LDF = TILE + 4;
+  __shared__ __attribute__((aligned(16))) float sF[NWAVES][TILE * LDF];   // each wavefront's F tile
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = wave_id();
+  const int n = lane & 31, h = lane >> 5;
+  const int groups = H / G;
+  const BlockXY bxy = xcd_block();
+  const int b = bxy.y / groups, gi = bxy.y % groups;
+  const int hd0 = gi * G;
+  const bool has_h0 = (gi == 0);
+  const int NBq = (Tq + TILE - 1) / TILE;
+  const int NKT = (Tk + TILE - 1) / TILE;
+  const int qsb = gridDim.x - 1 - bxy.x;
+  const int rb = qsb * NWAVES + wave;
+  const int q_rel = rb * TILE + n;
+  const int q_abs = q_off + q_rel;
+  const int64_t seq_row = (int64_t)b * H;
+  auto q_head = [&](int hh) -> const elem* {
+    if constexpr (CV) return q + (seq_row + hh) * Tq * D;
+    else return q + qs.at(b, hh);
+  };
+  auto k_head = [&](int hh) -> const elem* {
+    if constexpr (CV) return k + (seq_row + hh) * ks.head;
+    else return k + ks.at(b, hh);
+  };
+  const int64_t q_ld = CV ? (int64_t)D : (int64_t)qs.row;
+  const int k_ld = CV ? D : (int)ks.row;
+
+  auto kt_end_of = [&](int rbw) {
+    const int last = q_off + rbw * TILE + TILE - 1;
+    return min(last / TILE + 1, NKT);
+  };
+  const int my_end = (rb < NBq) ? kt_end_of(rb) : 0;
+  const int wg_end = kt_end_of(min(qsb * NWAVES + NWAVES - 1, NBq - 1));
+
+  // Q fragments (B operand of K Q^T): lane holds query q_rel.
+  frag qf[G][NS];
+  frag q0f[NS];
+#pragma unroll
+  for (int g = 0; g < G; ++g) {
+    const elem* qh = q_head(hd0 + g);
+#pragma unroll
+    for (int s = 0; s < NS; ++s) qf[g][s] = ld_std_bounded<OP>(qh, q_ld, q_rel, Tq, h, s);
+  }
+  if (!has_h0) {
+    const elem* qh = q_head(0);
+#pragma unroll
+    for (int s = 0; s < NS; ++s) q0f[s] = ld_std_bounded<OP>(qh, q_ld, q_rel, Tq, h, s);
+  }
+
+  float m[G], l[G];
+  f32x16 o[G][DB];
+#pragma unroll
+  for (int g = 0; g < G; ++g) {
+    m[g] = -INFINITY;
+    l[g] = 0.f;
+#pragma unroll
+    for (int db = 0; db < DB; ++db) o[g][db] = zero16();
+  }
+  // F negated, in units of the unscaled logit q.k (see fwd_kernel)
+  const float sl2 = scale * LOG2E;
+  const float neg_inv_scale = -1.f / scale;
+  float damp = 1.f;
+  if (damp_mode != 0) {
+    damp = fminf(1.f, train_len / (float)(q_abs + 1));
+    if (damp_mode == 2) damp = sqrtf(damp);
+  }
+
+  // key-side sources and this lane's parts of the direct loads
+  const __amdgpu_buffer_rsrc_t rs_k0 = rsrc(k_head(hd0), (int64_t)Tk * k_ld * 2);
+  const __amdgpu_buffer_rsrc_t rs_k1 = rsrc(k_head(hd0 + 1), (int64_t)Tk * k_ld * 2);
+  const __amdgpu_buffer_rsrc_t rs_kh = rsrc(k_head(0), (int64_t)Tk * k_ld * 2);
+  const __amdgpu_buffer_rsrc_t rs_v0 = rsrc(vt + (seq_row + hd0) * D * ldv, (int64_t)D * ldv * 2);
+  const __amdgpu_buffer_rsrc_t rs_v1 = rsrc(vt + (seq_row + hd0 + 1) * D * ldv, (int64_t)D * ldv * 2);
+  // this wavefront's carry row (its query block's; keys past the end read zero)
+  const __amdgpu_buffer_rsrc_t rs_c =
+      rsrc(carry + ((int64_t)b * NBq + min(rb, NBq - 1)) * Tk, (int64_t)Tk * 4);
+  const RowsLane rl_k(k_ld, lane);
+  const int cl = cols_lane(ldv, lane);
+
+  // everything key tile kt needs, into buffer B, by direct loads only (see bwd_kv64_kernel)
+  auto load_tile = [&](int kt, FwdTileBuf64& B) {
+    const int kbase = kt * TILE;
+    g2l_rows64(B.k[0], rs_k0, rl_k, k_ld, kbase, wave);
+    g2l_rows64(B.k[1], rs_k1, rl_k, k_ld, kbase, wave);
+    if (!has_h0) g2l_rows64(B.k[2], rs_kh, rl_k, k_ld, kbase, wave);
+    g2l_cols32(B.vt[0], rs_v0, cl, (int)ldv, kbase, wave);
+    g2l_cols32(B.vt[1], rs_v1, cl, (int)ldv, kbase, wave);
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(rs_c, (lds_void_ptr)B.c[wave], 4, (kbase + n) * 4, 0, 0, 0);
+  };
+  auto rfrag = [&](const elem* tile, int s) -> frag {
+    return *reinterpret_cast<const frag*>(tile + swz64(n, 2 * s + h));
+  };
+
+  load_tile(wg_end - 1, sB0);
+  wait_loads();
+  __syncthreads();
+
+  // one key tile (buffer t mod 2, named by ODD); INTERIOR and DAMP as in fwd_kernel
+  auto tile_step = [&](int t, auto interior_tag, auto damp_tag, auto odd_tag) __attribute__((always_inline)) {
+    constexpr bool INTERIOR = decltype(interior_tag)::value;
+    constexpr bool DAMP = decltype(damp_tag)::value;
+    constexpr bool ODD = decltype(odd_tag)::value;
+    FwdTileBuf64& B = ODD ? sB1 : sB0;
+    const int kt = wg_end - 1 - t;
+    if (t + 1 < wg_end) load_tile(kt - 1, ODD ? sB0 : sB1);   // free since the last barrier
+    if (kt < my_end) {   // (a wavefront past the last query block has none)
+      const int kbase = kt * TILE;
+      const bool edge =
+          !INTERIOR && ((kbase + TILE - 1 >= q_off + rb * TILE) || (kbase + TILE > Tk) || kbase < exempt);
+      auto body = [&]() {
+        // head 0's logits as (queries x keys), lane = key; -F through this wavefront's LDS rows
+        f32x16 l0t = zero16();
+        {
+          const elem* k0s = has_h0 ? B.k[0] : B.k[2];
+#pragma unroll
+          for (int s = 0; s < NS; ++s) l0t = OP::mma(has_h0 ? qf[0][s] : q0f[s], rfrag(k0s, s), l0t);
+        }
+        {
+          f32x16 sel;
+#pragma unroll
+          for (int i = 0; i < 16; ++i) sel[i] = __builtin_amdgcn_fmed3f(-l0t[i], -3.0e38f, 0.f);
+          if (edge) {
+            const int jk = kbase + n;
+            const int thr = jk >= exempt ? jk - (q_off + rb * TILE) - 4 * h : 32;
+#pragma unroll
+            for (int i = 0; i < 16; ++i) sel[i] = crow(i, 0) > thr ? sel[i] : 0.f;
+          }
+          float run = B.c[wave][n] * neg_inv_scale;
+          float* fw = sF[wave];
+#pragma unroll
+          for (int a = 0; a < 4; ++a) {
+            const Halves g = halves(((sel[4 * a] + sel[4 * a + 1]) + sel[4 * a + 2]) + sel[4 * a + 3]);
+            float p = (h == 0) ? run : run + g.lo;
+#pragma unroll
+            for (int t2 = 0; t2 < 4; ++t2) {
+              fw[crow(4 * a + t2, h) * LDF + n] = p;
+              p += sel[4 * a + t2];
+            }
+            run = (run + g.lo) + g.hi;
+          }
+        }
+        lds_wave_sync();
+        f32x16 fs;
+#pragma unroll
+        for (int a = 0; a < 4; ++a) {
+          const float4 f4 = *reinterpret_cast<const float4*>(&sF[wave][n * LDF + 8 * a + 4 * h]);
+          fs[4 * a] = f4.x;
+          fs[4 * a + 1] = f4.y;
+          fs[4 * a + 2] = f4.z;
+          fs[4 * a + 3] = f4.w;
+        }
+        if constexpr (DAMP) {
+#pragma unroll
+          for (int i = 0; i < 16; ++i) fs[i] *= damp;
+        }
+#pragma unroll
+        for (int g = 0; g < G; ++g) {
+          f32x16 lg = fs;   // the product accumulates onto -F: lg = q.k - F/s
+#pragma unroll
+          for (int s = 0; s < NS; ++s) lg = OP::mma(rfrag(B.k[g], s), qf[g][s], lg);
+          if (edge) {
+            const int thr = min(q_abs, Tk - 1) - kbase - 4 * h;
+#pragma unroll
+            for (int i = 0; i < 16; ++i) lg[i] = crow(i, 0) <= thr ? lg[i] : -INFINITY;
+          }
+          float zmax = -INFINITY;
+#pragma unroll
+          for (int i = 0; i < 16; ++i) zmax = fmaxf(zmax, lg[i]);
+          const Halves zh = halves(zmax);
+          const float m_new = fmaxf(m[g], fmaxf(zh.lo, zh.hi) * sl2);
+          if (__any(m_new > m[g])) {
+            const float alpha = (m_new == -INFINITY) ? 1.f : fast_exp2(m[g] - m_new);
+            m[g] = m_new;
+            l[g] *= alpha;
+#pragma unroll
+            for (int db = 0; db < DB; ++db)
+#pragma unroll
+              for (int i = 0; i < 16; ++i) o[g][db][i] *= alpha;
+          }
+          const float mu = (m[g] == -INFINITY) ? 0.f : m[g];
+          float psum = 0.f;
+#pragma unroll
+          for (int i = 0; i < 16; ++i) {
+            const float p = fast_exp2(fmaf(lg[i], sl2, -mu));
+            lg[i] = p;
+            psum += p;
+          }
+          l[g] += psum;
+          frag pf[AS];
+#pragma unroll
+          for (int s = 0; s < AS; ++s) pf[s] = OP::from_acc(lg, s);
+#pragma unroll
+          for (int db = 0; db < DB; ++db)
+#pragma unroll
+            for (int s = 0; s < AS; ++s)
+              o[g][db] = OP::mma(*reinterpret_cast<const frag*>(B.vt[g] + swz32(db * 32 + n, 2 * s + h)), pf[s],
+                                 o[g][db]);
+        }
+      };
+      body();
+    }
+    wait_loads();
+    __syncthreads();   // the next tile's operands are in; every wavefront is done with this one
+  };
+  const int i_lo = min((exempt + TILE - 1) / TILE, wg_end);
+  const int i_hi = max(i_lo, min(min(q_off + qsb * NWAVES * TILE, Tk) / TILE, wg_end));
+  auto sweep = [&](auto damp_tag) {
+    auto run = [&](int t0, int t1, auto interior_tag) {
+      int t = t0;
+      if (t < t1 && (t & 1)) tile_step(t++, interior_tag, damp_tag, std::true_type{});
+      for (; t + 1 < t1; t += 2) {
+        tile_step(t, interior_tag, damp_tag, std::false_type{});
+        tile_step(t + 1, interior_tag, damp_tag, std::true_type{});
+      }
+      if (t < t1) tile_step(t, interior_tag, damp_tag, std::false_type{});
+    };
+    run(0, wg_end - i_hi, std::false_type{});
+    run(wg_end - i_hi, wg_end - i_lo, std::true_type{});
+    run(wg_end - i_lo, wg_end, std::false_type{});
+  };
+  if (damp_mode != 0) sweep(std::true_type{});
+  else sweep(std::false_type{});
+
+  if (rb >= NBq || q_rel >= Tq) return;
+#pragma unroll
+  for (int g = 0; g < G; ++g) {
+    const Halves lh = halves(l[g]);
+    const float ltot = lh.lo + lh.hi;
+    const float inv = 1.f / ltot;
+    const int64_t row = (seq_row + hd0 + g) * Tq + q_rel;
+    float* orow = out + row * D;
+    elem* yrow = y ? y + ys.at(b, hd0 + g) + (int64_t)q_rel * ys.row : nullptr;
+#pragma unroll
+    for (int db = 0; db < DB; ++db) {
+#pragma unroll
+      for (int a = 0; a < 4; ++a) {
+        float4 v4 = make_float4(o[g][db][4 * a] * inv, o[g][db][4 * a + 1] * inv, o[g][db][4 * a + 2] * inv,
+                                o[g][db][4 * a + 3] * inv);
+        const int d = db * 32 + 8 * a + 4 * h;
+        *reinterpret_cast<float4*>(orow + d) = v4;
+        if (yrow)
+          *reinterpret_cast<uint2*>(yrow + d) =
+              make_uint2((uint32_t)OP::to_elem(v4.x) | ((uint32_t)OP::to_elem(v4.y) << 16),
+                         (uint32_t)OP::to_elem(v4.z) | ((uint32_t)OP::to_elem(v4.w) << 16));
+      }
+    }
+    if (h == 0) {
+      rmax[row] = m[g];
+      rden[row] = ltot;
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------------------------
 // Backward preparation: lse = rmax + log2(rden), ndbar = -rowsum(dO * O) (negated: the dO.v
 // products accumulate onto it), and the transposed copies Q^T, dO^T, K^T (R, D, ldt). The
 // statistics are laid out (R, ldt), each head's rows padded to ldt with lse = +inf (P = 0) and
@@ -2791,6 +3069,16 @@ void launch_fwd(const FwdCall& c, const typename OP::elem* vt, int64_t ldv) {
   const bool cv = c.qs.row == D && c.qs.head == (int64_t)c.Tq * D && c.qs.seq == (int64_t)c.H * c.qs.head &&
                   c.ks.row == D && c.ks.seq == (int64_t)c.H * c.ks.head;
   TimedLaunch timed(SA_KERNEL_FORWARD, c.st);
+  if constexpr (sizeof(elem) == 2 && D == 64 && G == 2) {   // the direct-load kernel
+#define SA_LAUNCH_FWD64(CVV)                                                                                      \
+  hipLaunchKernelGGL((fwd64_kernel<CVV>), grid, dim3(NTHREADS), 0, c.st, static_cast<const elem*>(c.q),          \
+                     static_cast<const elem*>(c.k), vt, c.carry, c.out, c.rmax, c.rden, static_cast<elem*>(c.y),  \
+                     c.ys, c.H, c.Tq, c.Tk, c.qs, c.ks, c.q_off, ldv, c.exempt, c.scale, c.damp_mode, c.train_len)
+    if (cv) SA_LAUNCH_FWD64(true);
+    else SA_LAUNCH_FWD64(false);
+#undef SA_LAUNCH_FWD64
+    return;
+  }
 #define SA_LAUNCH_FWD(CVV)                                                                                        \
   hipLaunchKernelGGL((fwd_kernel<OP, D, G, CVV>), grid, dim3(NTHREADS), 0, c.st, static_cast<const elem*>(c.q),  \
                      static_cast<const elem*>(c.k), vt, c.carry, c.out, c.rmax, c.rden, static_cast<elem*>(c.y),  \
@@ -2805,11 +3093,14 @@ int forward_impl(const FwdCall& c) {
   using elem = typename OP::elem;
   const int64_t ldv = sa_transposed_ld(c.Tk);
   elem* vt = static_cast<elem*>(c.ws);
-  launch_transpose<elem, D>(static_cast<const elem*>(c.v), vt, c.Tk, ldv, c.vs, c.H, (int64_t)c.nseq * c.H, c.st);
-  int rc = run_selection<OP, D>(c, c.st);
-  if (rc) return rc;
   const int dtype = sizeof(elem) == 2 ? SA_DTYPE_BF16 : SA_DTYPE_F32;
   const int G = auto_group(dtype, D, c.H, c.group, false);
+  // V^T in the column order of fwd64_kernel's direct loads when it runs
+  const bool crow = sizeof(elem) == 2 && D == 64 && G == 2;
+  launch_transpose<elem, D>(static_cast<const elem*>(c.v), vt, c.Tk, ldv, c.vs, c.H, (int64_t)c.nseq * c.H, c.st,
+                            crow);
+  int rc = run_selection<OP, D>(c, c.st);
+  if (rc) return rc;
   if (G == 4) {
     if constexpr (sizeof(elem) == 2 && D <= 64) launch_fwd<OP, D, 4>(c, vt, ldv);
   } else if (G == 2) {
