@@ -64,6 +64,39 @@ def test_forward_past_the_int32_offset_limit(cuda):
     torch.testing.assert_close(aux["selected_total"].double(), total, atol=1e-2, rtol=1e-3)
 
 
+def test_bf16_fwd_bwd_past_the_int32_offset_limit(cuda):
+    """The bf16 kernels at head dim 64 (direct loads into LDS) at T = 270,000, where CARRY's and the
+    checkpoint planes' element offsets pass 2^31: the last queries against the oracle's tail, finite
+    gradients, and the last key's dV, which only the last query attends: P[T-1, T-1] dO[T-1]."""
+    seq, heads = 270_000, 2
+    print(f"case bf16 fwd+bwd T={seq}", flush=True)
+    g = torch.Generator(device=cuda).manual_seed(32)
+    q, k, v = (torch.randn(1, heads, seq, 64, device=cuda, generator=g).bfloat16().requires_grad_(True)
+               for _ in range(3))
+    out = kernels.selective_attention(q, k, v)
+    dout = torch.randn(out.shape, device=cuda, generator=g)
+    dq, dk, dv = torch.autograd.grad(out, (q, k, v), dout)
+    rows, want, total = sa_oracle.tail(q.detach().double(), k.detach().double(), v.detach().double(), 64,
+                                       chunk=8192)
+    err = (out[:, :, rows].detach().double() - want).abs().max().item()
+    print(f"tail max-abs {err:.2e}", flush=True)
+    assert err < 2e-2
+    assert all(torch.isfinite(x).all() for x in (dq, dk, dv))
+    # the last row's weight on its own key: its logits less the history every key gathered from the
+    # earlier queries (the totals less the last query's own selection)
+    qd, kd = q.detach().double(), k.detach().double()
+    lg = sa_oracle.raw_logits(qd[:, :, -1:], kd)                          # (1, H, 1, T)
+    own = sa_oracle.selection(qd[:, :, -1:], kd, 1, q_offset=seq - 1)     # (1, 1, T)
+    hist = total - own[:, 0]                                              # (1, T)
+    p = torch.softmax(lg - hist[:, None, None, :], dim=-1)[..., -1]       # (1, H, 1)
+    want_dv = p[..., None] * dout[:, :, -1:].double()
+    got_dv = dv[:, :, -1:].double()
+    scale = want_dv.abs().max().item()
+    rel = ((got_dv - want_dv).abs().max() / scale).item()
+    print(f"last-key dV rel {rel:.2e}", flush=True)
+    assert rel < 2e-2
+
+
 def test_c3_training_step_d1024_16384(cuda):
     """C3: one full training step (forward, backward, clipping, fused AdamW) of the 24-layer
     d1024 / 16-head decoder on 1 x 16,384 tokens under bf16 autocast: the loss and every gradient
