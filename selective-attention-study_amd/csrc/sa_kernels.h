@@ -585,7 +585,9 @@ __global__ __launch_bounds__(NTHREADS) void sel_colsum_kernel(
   __syncthreads();
   for (int rb = rb0; rb < rb_end; ++rb) {
     const int buf = (rb - rb0) & 1;
-    if (rb + 1 < rb_end) nQ.load(q0, qs.row, (rb + 1) * TILE, Tq, tid);   // the next block, into registers
+    // the next block, into registers, unconditionally (past the end it reads zero rows, unused): a
+    // conditional load made the compiler wait for it at the join before this block's products
+    nQ.load(q0, qs.row, (rb + 1) * TILE, Tq, tid);
     float cs = 0.f;
     const int qbase = q_off + rb * TILE;   // absolute position of the block's first query
     // the tile holds a selectable pair only if some query is after the first key
