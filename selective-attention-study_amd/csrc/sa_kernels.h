@@ -1396,10 +1396,11 @@ void launch_transpose(const E* in, E* outT, int T, int64_t ldt, const Strides& i
 }
 
 // ---------------------------------------------------------------------------------------------
-// Backward kernel shapes. Each tile is loaded, stored to LDS and computed in turn (one LDS buffer):
-// a second workgroup on the CU hides the load latency better than pipelining the loads would
-// (measured). Both sides fit two workgroups per CU at bf16 head dims <= 64: the key side's K and V
-// rows sit in LDS, the query side's Q and dO rows and row statistics in registers.
+// Backward kernel shapes of the generic instances (every storage type and head dim but bf16 at 64,
+// which bwd_kv64_kernel / bwd_dq64_kernel take): each tile is loaded into registers, stored to LDS
+// and computed in turn (one LDS buffer), the load latency left to the CU's other workgroup. Both
+// sides fit two workgroups per CU at bf16 head dims <= 64: the key side's K and V rows sit in LDS,
+// the query side's Q and dO rows and row statistics in registers.
 template <class OP, int D>
 constexpr int dq_min_blocks() { return (sizeof(typename OP::elem) == 2 && D <= 64) ? 2 : 1; }
 template <class OP, int D, int G>
@@ -1561,7 +1562,8 @@ __device__ __forceinline__ bool big_tile(const f32x16& x) {
 // Backward, key side. grid (ceil(T/128), nseq * H/G); wavefront w owns keys [x*128 + 32w, +32) of
 // heads [gi*G, gi*G+G) and sweeps the query tiles last to first, with K, V and the dK, dV sums in
 // registers. The selection suffix U (over this group's heads) is checkpointed on entry to every
-// query tile into ucheck[gi][b][qb][j] for the dQ kernel. Head 0's dK gets g = -gate*U from every
+// query tile, for the dQ kernel, into row qb (keys j < 32 (qb + 1)) of the (gi, b) plane of ucheck,
+// a lower-triangular plane of rows laid end to end (utri_row). Head 0's dK gets g = -gate*U from every
 // group: the group holding head 0 folds it into head 0's dz; the others add their share to dk0x.
 
 // CV: every view is the contiguous (nseq, H, T, D) layout of sa_backward (see fwd_kernel).
