@@ -545,6 +545,32 @@ __device__ __forceinline__ float excl_scan32(float x) {
 }
 
 // ---------------------------------------------------------------------------------------------
+// One key block's selection summed over a query block: acc holds the raw logits (queries x keys, C
+// layout, lane = key j; element i is the block's query crow(i, h)), relu'd in unscaled logit units
+// (relu(s x) = s relu(x), s > 0); on tiles that are not interior, only the pairs with
+// exempt <= j < query count: crow(i, 0) > thr, thr = j - (first query of the block) - 4h (32 when j
+// is exempt). Queries past the end and keys past the end hold zero rows, so their logits add
+// nothing. Summed in a fixed tree order, the wavefront's halves added, times the scale (the same
+// value in both lanes of key j). The column-sum and one-pass carry kernels both take it, so their
+// sums agree bit for bit.
+__device__ __forceinline__ float block_selection_sum(const f32x16& acc, bool interior, int thr, float scale) {
+  f32x16 s;
+#pragma unroll
+  for (int i = 0; i < 16; ++i) s[i] = __builtin_amdgcn_fmed3f(acc[i], 0.f, 3.0e38f);
+  if (!interior) {
+#pragma unroll
+    for (int i = 0; i < 16; ++i) s[i] = crow(i, 0) > thr ? s[i] : 0.f;
+  }
+  float p[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) p[i] = s[2 * i] + s[2 * i + 1];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) p[i] = p[2 * i] + p[2 * i + 1];
+  const Halves cs = halves((p[0] + p[1]) + (p[2] + p[3]));
+  return (cs.lo + cs.hi) * scale;
+}
+
+// ---------------------------------------------------------------------------------------------
 // Selection column sums: colsum[b][rb][j] = sum over the queries r of block rb (chunk-relative)
 // of S[r, j]. One wavefront per key block (its K rows in registers); a workgroup walks RB query
 // blocks, each staged once in LDS for its four wavefronts while the next one loads.
@@ -595,21 +621,8 @@ __global__ __launch_bounds__(NTHREADS) void sel_colsum_kernel(
       f32x16 acc = zero16();
 #pragma unroll
       for (int s = 0; s < NS; ++s) acc = OP::mma(OP::ld_std(sQ[buf], LDK, n, h, s), kf[s], acc);
-      // relu in unscaled logit units (relu(s x) = s relu(x), s > 0); the scale enters once
-      const bool interior = qbase > kbase + TILE - 1 && kbase >= exempt && rb * TILE + TILE <= Tq;
-      if (interior) {
-#pragma unroll
-        for (int i = 0; i < 16; ++i) cs += __builtin_amdgcn_fmed3f(acc[i], 0.f, 3.0e38f);
-      } else {
-#pragma unroll
-        for (int i = 0; i < 16; ++i) {
-          const int r = rb * TILE + crow(i, h);
-          const bool gate = (r < Tq) && (j >= exempt) && (j < q_off + r) && (acc[i] > 0.f);
-          cs += gate ? acc[i] : 0.f;
-        }
-      }
-      cs += xor32(cs);
-      cs *= scale;
+      const bool interior = qbase > kbase + TILE - 1 && kbase >= exempt;
+      cs = block_selection_sum(acc, interior, j >= exempt ? j - qbase - 4 * h : 32, scale);
     }
     if (kb < NKT && h == 0 && j < Tk) colsum[((int64_t)b * NBq + rb) * Tk + j] = cs;
     if (rb + 1 < rb_end) nQ.template store<LDK>(sQ[buf ^ 1], tid);
@@ -645,6 +658,141 @@ __global__ __launch_bounds__(NTHREADS) void sel_scan_kernel(
     run += c;
   }
   state_out[(int64_t)b * state_ld + j] = run;
+}
+
+// The selection carry in one pass, for bf16 storage at head dim 64 when the call has sequences
+// enough to fill the GPU (the per-head mode: every head its own sequence). grid
+// (ceil(NKT/(4 KPW)), nseq): wavefront w owns key blocks (4x + w) KPW + u, u < KPW (their K rows in
+// registers, one read of each query fragment serving all of them), and the workgroup walks the
+// query blocks from the first that can select one of its keys to the last, each staged once into
+// LDS by direct loads issued NBUF - 1 blocks ahead (NBUF buffers, one barrier per block), keeping
+// each key's running selection in a register. carry[b][rb][j] is stored on entry to block rb (the
+// rows before the first block hold the entering value, state_in or zero, as the scan writes them)
+// and state_out[b][j] after the last. Each block's sum is block_selection_sum, as in the column-sum
+// kernel, and the sums are added in the scan's order: both paths give the same bits, without the
+// column sums' round trip through HBM.
+//
+// Every block issues the same vector-memory operations -- KPW carry stores through a buffer
+// resource (lanes that own no key aim past its end, where the store is dropped) and one query-block
+// load (past the last block: zero rows into a buffer nobody reads) -- so a fixed count
+// vmcnt((NBUF - 2) (KPW + 1)) at the end of a block waits exactly for the next block's load (the
+// counter drains in issue order).
+constexpr int SEL_CARRY_KPW = 1;             // key blocks per wavefront
+constexpr int SEL_CARRY_NBUF = 4;            // query-block buffers
+constexpr int SEL_CARRY_MIN_BLOCKS = 2048;   // workgroups below which the two-kernel path runs
+
+__global__ __launch_bounds__(NTHREADS) void sel_carry64_kernel(
+    const uint16_t* __restrict__ q, const uint16_t* __restrict__ k, float* __restrict__ carry,
+    const float* state_in, float* state_out, int64_t state_ld, int Tq, int Tk, Strides qs, Strides ks, int q_off,
+    int exempt, float scale) {
+  using OP = OpBF16;
+  using frag = OP::frag;
+  constexpr int D = 64, NS = 4, KPW = SEL_CARRY_KPW, NBUF = SEL_CARRY_NBUF, AHEAD = NBUF - 1;
+  static_assert(NBUF == 4, "the block loop names four buffers");
+  // separate LDS variables, named at compile time, so the compiler knows a block's reads do not
+  // touch the buffers the direct loads are filling
+  __shared__ __attribute__((aligned(16))) uint16_t sQ0[TILE * D];
+  __shared__ __attribute__((aligned(16))) uint16_t sQ1[TILE * D];
+  __shared__ __attribute__((aligned(16))) uint16_t sQ2[TILE * D];
+  __shared__ __attribute__((aligned(16))) uint16_t sQ3[TILE * D];
+  auto sbuf = [&](auto idx) -> uint16_t* {
+    constexpr int I = decltype(idx)::value % NBUF;
+    if constexpr (I == 0) return sQ0;
+    else if constexpr (I == 1) return sQ1;
+    else if constexpr (I == 2) return sQ2;
+    else return sQ3;
+  };
+  const int tid = threadIdx.x, lane = tid & 63, wave = wave_id();
+  const int n = lane & 31, h = lane >> 5;
+  const int NKT = (Tk + TILE - 1) / TILE;
+  const int NBq = (Tq + TILE - 1) / TILE;
+  const BlockXY bxy = xcd_block();   // each XCD takes whole sequences: their query rows stay in its L2
+  const int b = bxy.y;
+  const int kb0 = bxy.x * (NWAVES * KPW);
+  const uint16_t* q0 = q + qs.at(b, 0);
+  const uint16_t* k0 = k + ks.at(b, 0);
+  float* plane = carry + (int64_t)b * NBq * Tk;
+  const int plane_bytes = NBq * Tk * 4;   // below 2 GiB (the launch checks)
+  const __amdgpu_buffer_rsrc_t rs_c = rsrc(plane, plane_bytes);
+
+  // per key block u of the wavefront (blocks past the last one only stage): key j, whether this
+  // lane stores key j's values (and the byte offset its stores take: past the plane if not), its
+  // K rows, its running selection
+  int kb[KPW], jj[KPW], voff[KPW];
+  bool owner[KPW];
+  frag kf[KPW][NS];
+  float run[KPW];
+#pragma unroll
+  for (int u = 0; u < KPW; ++u) {
+    kb[u] = kb0 + wave * KPW + u;
+    jj[u] = kb[u] * TILE + n;
+    owner[u] = kb[u] < NKT && h == 0 && jj[u] < Tk;
+    voff[u] = owner[u] ? jj[u] * 4 : plane_bytes;
+#pragma unroll
+    for (int s = 0; s < NS; ++s) kf[u][s] = ld_std_bounded<OP>(k0, ks.row, jj[u], Tk, h, s);
+    run[u] = (state_in != nullptr && jj[u] < q_off && jj[u] < Tk) ? state_in[(int64_t)b * state_ld + jj[u]] : 0.f;
+  }
+
+  // blocks before rb_lo end before the workgroup's first key: no pair of theirs is selectable
+  const int lead = kb0 * TILE - q_off;
+  const int rb_lo = min(lead > 0 ? lead / TILE : 0, NBq);
+#pragma unroll
+  for (int u = 0; u < KPW; ++u)
+    if (owner[u])
+      for (int rb = 0; rb < rb_lo; ++rb) plane[(int64_t)rb * Tk + jj[u]] = run[u];
+
+  const int q_ld = (int)qs.row;
+  const __amdgpu_buffer_rsrc_t rs_q = rsrc(q0, (int64_t)Tq * q_ld * 2);   // rows past Tq read zero
+  const RowsLane rl_q(q_ld, lane);
+  const int nb = NBq - rb_lo;   // blocks walked; block rb_lo + t sits in buffer t mod NBUF
+  g2l_rows64(sQ0, rs_q, rl_q, q_ld, rb_lo * TILE, wave);
+  g2l_rows64(sQ1, rs_q, rl_q, q_ld, (rb_lo + 1) * TILE, wave);
+  g2l_rows64(sQ2, rs_q, rl_q, q_ld, (rb_lo + 2) * TILE, wave);
+  wait_loads();
+  __syncthreads();
+
+  auto step = [&](int t, auto buf_tag) {
+    constexpr int BUF = decltype(buf_tag)::value;
+    const int rb = rb_lo + t;
+#pragma unroll
+    for (int u = 0; u < KPW; ++u)   // the value on entry to the block
+      __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(run[u]), rs_c, voff[u], rb * Tk * 4, 0);
+    g2l_rows64(sbuf(std::integral_constant<int, BUF + AHEAD>{}), rs_q, rl_q, q_ld, (rb + AHEAD) * TILE, wave);
+    const uint16_t* sQ = sbuf(buf_tag);
+    const int qbase = q_off + rb * TILE;
+    frag qa[NS];
+#pragma unroll
+    for (int s = 0; s < NS; ++s) qa[s] = *reinterpret_cast<const frag*>(sQ + swz64(n, 2 * s + h));
+#pragma unroll
+    for (int u = 0; u < KPW; ++u) {
+      const int kbase = kb[u] * TILE;
+      if (kb[u] < NKT && qbase + TILE - 1 > kbase) {
+        f32x16 acc = zero16();
+#pragma unroll
+        for (int s = 0; s < NS; ++s) acc = OP::mma(qa[s], kf[u][s], acc);
+        const bool interior = qbase > kbase + TILE - 1 && kbase >= exempt;
+        run[u] += block_selection_sum(acc, interior, jj[u] >= exempt ? jj[u] - qbase - 4 * h : 32, scale);
+      }
+    }
+    // The next block's load is in (the loads and stores issued after it may still run), this
+    // block's LDS reads are done, then the barrier: as one asm block, since before a compiler-seen
+    // barrier the compiler waits for every direct load into LDS, the ones ahead included.
+    __asm__ volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)\n\ts_barrier" ::"n"((AHEAD - 1) * (KPW + 1)) : "memory");
+  };
+  int t = 0;
+  for (; t + 3 < nb; t += 4) {
+    step(t, std::integral_constant<int, 0>{});
+    step(t + 1, std::integral_constant<int, 1>{});
+    step(t + 2, std::integral_constant<int, 2>{});
+    step(t + 3, std::integral_constant<int, 3>{});
+  }
+  if (t < nb) step(t, std::integral_constant<int, 0>{});
+  if (t + 1 < nb) step(t + 1, std::integral_constant<int, 1>{});
+  if (t + 2 < nb) step(t + 2, std::integral_constant<int, 2>{});
+  wait_loads();   // nothing may be left in flight into LDS when the workgroup ends
+#pragma unroll
+  for (int u = 0; u < KPW; ++u)
+    if (owner[u]) state_out[(int64_t)b * state_ld + jj[u]] = run[u];
 }
 
 // ---------------------------------------------------------------------------------------------
@@ -3059,9 +3207,19 @@ template <class OP, int D>
 int run_selection(const FwdCall& c, hipStream_t st) {
   using elem = typename OP::elem;
   const int NBq = (int)cdiv(c.Tq, TILE), NKT = (int)cdiv(c.Tk, TILE);
+  TimedLaunch timed(SA_KERNEL_SELECTION, st);
+  if constexpr (sizeof(elem) == 2 && D == 64) {
+    const int64_t wgs = cdiv(NKT, NWAVES * SEL_CARRY_KPW);
+    // (its carry stores address one sequence's plane through a 32-bit buffer range)
+    if (wgs * c.nseq >= SEL_CARRY_MIN_BLOCKS && (int64_t)NBq * c.Tk * 4 < ((int64_t)1 << 31)) {
+      hipLaunchKernelGGL(sel_carry64_kernel, dim3((unsigned)wgs, (unsigned)c.nseq), dim3(NTHREADS), 0,
+                         st, static_cast<const uint16_t*>(c.q), static_cast<const uint16_t*>(c.k), c.carry,
+                         c.state_in, c.state_out, c.state_ld, c.Tq, c.Tk, c.qs, c.ks, c.q_off, c.exempt, c.scale);
+      return launch_status();
+    }
+  }
   const int RB = SEL_RB;
   dim3 g1((unsigned)cdiv(NKT, NWAVES), (unsigned)cdiv(NBq, RB), (unsigned)c.nseq);
-  TimedLaunch timed(SA_KERNEL_SELECTION, st);
   hipLaunchKernelGGL((sel_colsum_kernel<OP, D>), g1, dim3(NTHREADS), 0, st, static_cast<const elem*>(c.q),
                      static_cast<const elem*>(c.k), c.carry, c.H, c.Tq, c.Tk, c.qs, c.ks, c.q_off, c.exempt, c.scale,
                      RB);
