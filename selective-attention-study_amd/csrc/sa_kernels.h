@@ -660,8 +660,9 @@ __global__ __launch_bounds__(NTHREADS) void sel_scan_kernel(
   state_out[(int64_t)b * state_ld + j] = run;
 }
 
-// The selection carry in one pass, for bf16 storage at head dim 64 when the call has sequences
-// enough to fill the GPU (the per-head mode: every head its own sequence). grid
+// The selection carry in one pass, for bf16 storage at head dim 64 when the call has key blocks
+// enough for a workgroup per CU (many sequences, as in the per-head mode where every head is its own
+// sequence, or a long key range, as in the later chunks of a chunked prefill). grid
 // (ceil(NKT/(4 KPW)), nseq): wavefront w owns key blocks (4x + w) KPW + u, u < KPW (their K rows in
 // registers, one read of each query fragment serving all of them), and the workgroup walks the
 // query blocks from the first that can select one of its keys to the last, each staged once into
@@ -679,7 +680,7 @@ __global__ __launch_bounds__(NTHREADS) void sel_scan_kernel(
 // counter drains in issue order).
 constexpr int SEL_CARRY_KPW = 1;             // key blocks per wavefront
 constexpr int SEL_CARRY_NBUF = 4;            // query-block buffers
-constexpr int SEL_CARRY_MIN_BLOCKS = 2048;   // workgroups below which the two-kernel path runs
+constexpr int SEL_CARRY_MIN_BLOCKS = 256;    // workgroups below which the two-kernel path runs
 
 __global__ __launch_bounds__(NTHREADS) void sel_carry64_kernel(
     const uint16_t* __restrict__ q, const uint16_t* __restrict__ k, float* __restrict__ carry,
