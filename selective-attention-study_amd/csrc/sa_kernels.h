@@ -1698,8 +1698,9 @@ __device__ __forceinline__ void p_dz_tile_r(const f32x16& lg, const f32x16& dpb,
   for (int i = 0; i < 16; ++i) dz[i] = pr[i] * dpb[i];
 }
 
-// Whether some |g| of the wavefront's tile is large enough for the split-operand products: g sums
-// dz over every later query of the group's heads and can outgrow the dz tiles many times.
+// Whether some value of the wavefront's tile is large enough for the split-operand products (the
+// rounding of a bf16 operand then matters beside the others): g sums dz over every later query of
+// the group's heads and can outgrow the dz tiles many times. Taken on g, and on head 0's dz + g.
 __device__ __forceinline__ bool big_tile(const f32x16& x) {
   bool big = false;
 #pragma unroll
@@ -2254,7 +2255,7 @@ __global__ __launch_bounds__(NTHREADS, 2) void bwd_kv64_kernel(
           if constexpr (H0) {   // head 0's dK takes g with its own dz
 #pragma unroll
             for (int i = 0; i < 16; ++i) dz[i] += gp[i];
-            acc_t(dkt, B.t[0], dz, true);
+            acc_t(dkt, B.t[0], dz, split || big_tile(dz));
           } else {
             acc_t(dkt, B.t[0], dz, split);
             acc_t(dk0t, B.t[2], gp, big_tile(gp));
@@ -2584,7 +2585,7 @@ __global__ __launch_bounds__(NTHREADS, (dq_min_blocks<OP, D>())) void bwd_dq_ker
             f32x16 dzh;
   #pragma unroll
             for (int i = 0; i < 16; ++i) dzh[i] = dz0[i] + gp[i];
-            acc_xk(dqacc[0], dzh, sKt[0], true);
+            acc_xk(dqacc[0], dzh, sKt[0], big_tile(dzh));
           } else {
             acc_xk(dq0acc, gp, sKt[G], big_tile(gp));
           }
@@ -2830,7 +2831,7 @@ __global__ __launch_bounds__(DQ64_WAVES * 64, 1) void bwd_dq64_kernel(
         if constexpr (H0) {   // head 0's dQ takes g with its own dz
 #pragma unroll
           for (int i = 0; i < 16; ++i) dz[i] += gp[i];
-          acc_xk(dqacc, dz, B.kt[0], true);
+          acc_xk(dqacc, dz, B.kt[0], big_tile(dz));
         } else {
           acc_xk(dqacc, dz, B.kt[0], false);
           acc_xk(dq0acc, gp, B.kt[1], big_tile(gp));
