@@ -835,6 +835,7 @@ __global__ __launch_bounds__(NTHREADS, (fwd_min_blocks<OP, D, G>())) void fwd_ke
   __shared__ __attribute__((aligned(16))) float sC[NBUF][NWAVES][TILE];   // -carry rows, logit units
   constexpr int LDF = TILE + 4;
   __shared__ __attribute__((aligned(16))) float sF[NWAVES][TILE * LDF];   // each wavefront's F tile
+  __shared__ __attribute__((aligned(16))) float sDamp[NWAVES][TILE];      // its queries' damping factors
 
   const int tid = threadIdx.x, lane = tid & 63, wave = wave_id();
   const int n = lane & 31, h = lane >> 5;
@@ -903,6 +904,7 @@ __global__ __launch_bounds__(NTHREADS, (fwd_min_blocks<OP, D, G>())) void fwd_ke
     damp = fminf(1.f, train_len / (float)(q_abs + 1));
     if (damp_mode == 2) damp = sqrtf(damp);
   }
+  if (lane < TILE) sDamp[wave][lane] = damp;   // (read after the first barrier)
 
   // Staging of one key tile: K of the group (+ head 0's), V^T of the group, and the carry rows of
   // the workgroup's four query blocks (threads 0..127: wavefront w's row, key tid % 32).
@@ -997,9 +999,16 @@ __global__ __launch_bounds__(NTHREADS, (fwd_min_blocks<OP, D, G>())) void fwd_ke
           for (int a = 0; a < 4; ++a) {
             const Halves g = halves(((sel[4 * a] + sel[4 * a + 1]) + sel[4 * a + 2]) + sel[4 * a + 3]);
             float p = (h == 0) ? run : run + g.lo;   // rows 8a..8a+3 in the low half, 8a+4.. in the high
+            float4 dm = make_float4(1.f, 1.f, 1.f, 1.f);   // the rows' damping factors
+            if constexpr (DAMP) dm = *reinterpret_cast<const float4*>(&sDamp[wave][8 * a + 4 * h]);
+            const float dmv[4] = {dm.x, dm.y, dm.z, dm.w};
 #pragma unroll
             for (int t = 0; t < 4; ++t) {
-              fw[crow(4 * a + t, h) * LDF + n] = p;
+              // a one-head group holding head 0 sends that head's whole adjusted logit,
+              // q.k - damp F/s, so its (keys x queries) product is not taken again
+              float f = p;
+              if (G == 1 && has_h0) f = DAMP ? fmaf(dmv[t], p, l0t[4 * a + t]) : p + l0t[4 * a + t];
+              fw[crow(4 * a + t, h) * LDF + n] = f;
               p += sel[4 * a + t];
             }
             run = (run + g.lo) + g.hi;
@@ -1016,15 +1025,19 @@ __global__ __launch_bounds__(NTHREADS, (fwd_min_blocks<OP, D, G>())) void fwd_ke
           fs[4 * a + 3] = f4.w;
         }
         if constexpr (DAMP) {
+          if (G > 1 || !has_h0) {
 #pragma unroll
-          for (int i = 0; i < 16; ++i) fs[i] *= damp;
+            for (int i = 0; i < 16; ++i) fs[i] *= damp;
+          }
         }
 
 #pragma unroll
         for (int g = 0; g < G; ++g) {
           f32x16 lg = fs;   // the product accumulates onto -F: lg = q.k - F/s
+          if (G > 1 || !has_h0) {   // (else head 0's came through LDS whole)
 #pragma unroll
-          for (int s = 0; s < NS; ++s) lg = OP::mma(OP::ld_std(sK[buf][g], LDK, n, h, s), qf[g][s], lg);
+            for (int s = 0; s < NS; ++s) lg = OP::mma(OP::ld_std(sK[buf][g], LDK, n, h, s), qf[g][s], lg);
+          }
           if (edge) {   // keys j = kbase + crow(i, h) <= min(q_abs, Tk - 1)
             const int thr = min(q_abs, Tk - 1) - kbase - 4 * h;
 #pragma unroll
