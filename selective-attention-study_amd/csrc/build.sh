@@ -7,8 +7,13 @@
 #                its heuristics the compiler keeps them in AGPRs and copies every loop-carried
 #                accumulator back and forth each iteration), and the compiler's iterative ILP
 #                scheduler (faster for the tile loops than the default one)
-#   sa_bf16_kv.hip  the bf16 key-side backward kernel, the same flags, in a unit of its own (its
-#                template instances compile in parallel with the rest)
+#   sa_bf16_kv.hip  the bf16 key-side backward kernel at head dim 64 for sequences of several
+#                heads: accumulators in VGPRs, the default scheduler (2% faster there than the
+#                iterative one)
+#   sa_bf16_kv1.hip  the same kernel for one-head sequences (every workgroup in the head-0 loop),
+#                sa_bf16.hip's flags (4% faster there)
+#   sa_bf16_kvg.hip  the bf16 key-side instances at head dims 32 and 128: accumulators in VGPRs,
+#                the default scheduler (the two options together crash this compiler on them)
 #   sa_bf16_dec.hip  the bf16 decode-step kernels, the default scheduler (faster for them)
 #   sa_f32.hip   fp32-storage kernels, the compiler's own accumulator placement
 #   sa_abi.hip   the C ABI (host code only)
@@ -41,8 +46,12 @@ unit() {
 tuned=(-mllvm -amdgpu-mfma-vgpr-form -mllvm -amdgpu-sched-strategy=iterative-ilp)
 unit sa_bf16.hip sa_bf16.o "${tuned[@]}" &
 p1=$!
-unit sa_bf16_kv.hip sa_bf16_kv.o "${tuned[@]}" &
+unit sa_bf16_kv.hip sa_bf16_kv.o -mllvm -amdgpu-mfma-vgpr-form &
 p4=$!
+unit sa_bf16_kv1.hip sa_bf16_kv1.o "${tuned[@]}" &
+p7=$!
+unit sa_bf16_kvg.hip sa_bf16_kvg.o -mllvm -amdgpu-mfma-vgpr-form &
+p6=$!
 unit sa_bf16_dec.hip sa_bf16_dec.o -mllvm -amdgpu-mfma-vgpr-form &
 p5=$!
 unit sa_f32.hip sa_f32.o &
@@ -55,8 +64,10 @@ wait $p2 || rc=1
 wait $p3 || rc=1
 wait $p4 || rc=1
 wait $p5 || rc=1
+wait $p6 || rc=1
+wait $p7 || rc=1
 [ $rc -eq 0 ] || { echo "build.sh: a compile failed" >&2; exit 1; }
-hipcc --offload-arch=gfx950 -shared -fPIC "$tmp/sa_bf16.o" "$tmp/sa_bf16_kv.o" "$tmp/sa_bf16_dec.o" "$tmp/sa_f32.o" \
+hipcc --offload-arch=gfx950 -shared -fPIC "$tmp/sa_bf16.o" "$tmp/sa_bf16_kv.o" "$tmp/sa_bf16_kv1.o" "$tmp/sa_bf16_kvg.o" "$tmp/sa_bf16_dec.o" "$tmp/sa_f32.o" \
   "$tmp/sa_abi.o" \
   -o "$out.tmp"
 mv "$out.tmp" "$out"

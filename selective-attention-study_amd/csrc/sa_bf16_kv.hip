@@ -1,26 +1,20 @@
-// The key-side backward kernel's bf16-storage instances, in a translation unit of their own (built
-// with the flags of sa_bf16.hip, in parallel with it).
+// The key-side backward kernel's bf16-storage instances at head dim 64, in translation units of
+// their own, compiled in parallel with the rest. This unit (accumulators in VGPRs, the compiler's
+// default scheduler) serves sequences of several heads; sa_bf16_kv1.hip (with sa_bf16.hip's
+// iterative scheduler as well) the one-head sequences, whose workgroups all take the head-0 tile
+// loop, which that scheduler runs faster (measured: the loop of the other heads runs faster under
+// the default one). The other head dims' instances are in sa_bf16_kvg.hip.
 
 #include "sa_kernels.h"
 
 namespace sa_host {
 
 int launch_bwd_kv_bf16(int D, int G, bool cv, const KvLaunch& a) {
-#define SA_KV(DD, GG)                                        \
-  if (cv) launch_kv_from<OpBF16, DD, GG, true>(a);           \
-  else launch_kv_from<OpBF16, DD, GG, false>(a);             \
-  return launch_status()
-  if (D == 32) {
-    if (G == 2) { SA_KV(32, 2); }
-    SA_KV(32, 1);
-  }
-  if (D == 64) {   // one head per wavefront at head dim 64: the pipelined kernel
-    if (cv) launch_kv64_from<true>(a);
-    else launch_kv64_from<false>(a);
-    return launch_status();
-  }
-  SA_KV(128, 1);
-#undef SA_KV
+  if (D != 64) return launch_bwd_kv_bf16_generic(D, G, cv, a);
+  if (a.H == 1) return launch_bwd_kv64_solo(cv, a);
+  if (cv) launch_kv64_from<true>(a);
+  else launch_kv64_from<false>(a);
+  return launch_status();
 }
 
 }  // namespace sa_host

@@ -228,7 +228,9 @@ struct KvLaunch {
   float scale;
   hipStream_t st;
 };
-SA_HIDDEN int launch_bwd_kv_bf16(int D, int G, bool cv, const KvLaunch& a);   // sa_bf16_kv.hip
+SA_HIDDEN int launch_bwd_kv_bf16(int D, int G, bool cv, const KvLaunch& a);           // sa_bf16_kv.hip
+SA_HIDDEN int launch_bwd_kv_bf16_generic(int D, int G, bool cv, const KvLaunch& a);   // sa_bf16_kvg.hip
+SA_HIDDEN int launch_bwd_kv64_solo(bool cv, const KvLaunch& a);                       // sa_bf16_kv1.hip
 
 SA_HIDDEN int forward_bf16(const FwdCall& c);    // sa_bf16.hip
 SA_HIDDEN int backward_bf16(const BwdCall& c);

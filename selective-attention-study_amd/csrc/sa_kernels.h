@@ -2046,7 +2046,7 @@ __global__ __launch_bounds__(NTHREADS, (kv_min_blocks<OP, D, G>())) void bwd_kv_
                                       dkt[g][db][4 * a + 2] * scale, dkt[g][db][4 * a + 3] * scale);
         store_grad4(dvv, b, hh, j, d,
                     make_float4(dvt[g][db][4 * a], dvt[g][db][4 * a + 1], dvt[g][db][4 * a + 2], dvt[g][db][4 * a + 3]));
-        if (hh == 0) *reinterpret_cast<float4*>(dk0h + ((int64_t)b * T + j) * D + d) = kq;
+        if (hh == 0 && H > 1) *reinterpret_cast<float4*>(dk0h + ((int64_t)b * T + j) * D + d) = kq;
         else store_grad4(dkv, b, hh, j, d, kq);
       }
   }
@@ -2300,7 +2300,7 @@ __global__ __launch_bounds__(NTHREADS, 2) void bwd_kv64_kernel(
 
   if (j >= T) return;
   // dV and the dK of heads other than 0 go to the caller's views; head 0's dK to its fp32 sums,
-  // where the other heads' shares join it
+  // where the other heads' shares join it (to its view too when it is the sequence's only head)
 #pragma unroll
   for (int db = 0; db < DB; ++db)
 #pragma unroll
@@ -2309,7 +2309,7 @@ __global__ __launch_bounds__(NTHREADS, 2) void bwd_kv64_kernel(
       const float4 kq = make_float4(dkt[db][4 * a] * scale, dkt[db][4 * a + 1] * scale, dkt[db][4 * a + 2] * scale,
                                     dkt[db][4 * a + 3] * scale);
       store_grad4(dvv, b, hh, j, d, make_float4(dvt[db][4 * a], dvt[db][4 * a + 1], dvt[db][4 * a + 2], dvt[db][4 * a + 3]));
-      if (has_h0) *reinterpret_cast<float4*>(dk0h + ((int64_t)b * T + j) * D + d) = kq;
+      if (has_h0 && H > 1) *reinterpret_cast<float4*>(dk0h + ((int64_t)b * T + j) * D + d) = kq;
       else store_grad4(dkv, b, hh, j, d, kq);
     }
   if (!has_h0) {
@@ -2628,7 +2628,7 @@ __global__ __launch_bounds__(NTHREADS, (dq_min_blocks<OP, D>())) void bwd_dq_ker
       if (r < T) {
 #pragma unroll
         for (int db = 0; db < DB; ++db) {
-          if (hh == 0) dq0h[((int64_t)b * T + r) * D + db * 32 + n] = dqacc[g][db][i];
+          if (hh == 0 && H > 1) dq0h[((int64_t)b * T + r) * D + db * 32 + n] = dqacc[g][db][i];
           else store_grad1(dqv, b, hh, r, db * 32 + n, dqacc[g][db][i] * scale);
         }
       }
@@ -2875,14 +2875,14 @@ __global__ __launch_bounds__(DQ64_WAVES * 64, 1) void bwd_dq64_kernel(
 
   if (qb >= NB) return;
   // heads other than 0: dQ (scaled) to the caller's view; head 0: unscaled fp32 sums, where the
-  // other heads' shares join it
+  // other heads' shares join it (to its view too when it is the sequence's only head)
 #pragma unroll
   for (int i = 0; i < 16; ++i) {
     const int r = qbase + crow(i, h);
     if (r < T) {
 #pragma unroll
       for (int db = 0; db < DB; ++db) {
-        if (has_h0) dq0h[((int64_t)b * T + r) * D + db * 32 + n] = dqacc[db][i];
+        if (has_h0 && H > 1) dq0h[((int64_t)b * T + r) * D + db * 32 + n] = dqacc[db][i];
         else store_grad1(dqv, b, hh, r, db * 32 + n, dqacc[db][i] * scale);
       }
     }
@@ -2898,9 +2898,6 @@ __global__ __launch_bounds__(DQ64_WAVES * 64, 1) void bwd_dq64_kernel(
     }
   }
 }
-
-// Gradients to the output dtype (bf16 or fp32): dq*scale, dk, dv, with head 0's dQ and dK shares
-// from the other head groups (dq0x unscaled, dk0x scaled) added to head 0.
 
 // Head 0's gradients: its own fp32 sums plus the other groups' shares, (b, t, D) contiguous, four
 // elements per thread, to the caller's views.
@@ -3410,9 +3407,9 @@ int backward_impl(const BwdCall& c) {
   hipLaunchKernelGGL((bwd_rowstats_kernel<OP, D>), dim3((unsigned)cdiv(R * ldt * (D / 8), NTHREADS)),
                      dim3(NTHREADS), 0, st, dout, c.dos, H, T, c.out, c.rmax, c.rden, lse, dbar, ldt, R * ldt,
                      // head 0's shares from the other groups are atomic targets (one add per element
-                     // and group): cleared here
+                     // and group): cleared here (a one-head sequence has none)
                      reinterpret_cast<float4*>(dq0x), reinterpret_cast<float4*>(dk0x),
-                     (int64_t)nseq * T * D / 4);
+                     H > 1 ? (int64_t)nseq * T * D / 4 : 0);
   int rc = launch_status();   // the transposes and row statistics
   if (rc) return rc;
 #define SA_LAUNCH_BWD(GG) launch_bwd<OP, D, GG>(c, qt, kt, dot, lse, dbar, ucheck, dq0h, dk0h, dq0x, dk0x, ldt)
@@ -3423,6 +3420,7 @@ int backward_impl(const BwdCall& c) {
   }
 #undef SA_LAUNCH_BWD
   if (rc) return rc;
+  if (H == 1) return SA_OK;   // a one-head sequence's kernels wrote its gradients to the views
   // head 0's dQ, dK: its own sums plus the other groups' shares
   const int64_t total4 = (int64_t)nseq * T * D / 4;
   const int f32 = c.grad_dtype == SA_DTYPE_F32;
