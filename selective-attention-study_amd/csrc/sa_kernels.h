@@ -1132,14 +1132,22 @@ __global__ __launch_bounds__(NTHREADS, (fwd_min_blocks<OP, D, G>())) void fwd_ke
 
 // ---------------------------------------------------------------------------------------------
 // Forward, bf16 storage at head dim 64 with two heads per wavefront (the default there): fwd_kernel's
-// tile work with every key tile's operands -- the K rows of both heads and head 0's (swz64), their
-// V^T (swz32, written in C-layout column order by the transpose), and each wavefront's carry row
-// -- loaded straight into LDS one tile ahead, two buffers as separate LDS variables and the tile
-// loop run in pairs (see bwd_kv64_kernel); one barrier per tile.
+// tile work with every key tile's operands loaded straight into LDS ahead of use (see
+// bwd_kv64_kernel), and the selection one tile ahead of the softmax: while tile t's logit products,
+// softmax and value products run, the wavefront also takes head 0's logits of tile t + 1 and turns
+// them into that tile's F (through its LDS rows, read at the start of tile t + 1), so each tile is
+// one block of independent products and arithmetic the compiler interleaves, with no wait inside it
+// for the F round trip. The K rows of the two heads and their V^T (swz64 / swz32) load one tile ahead
+// into two buffers; head 0's K rows and each wavefront's carry row two tiles ahead into two more;
+// all four are separate LDS variables and the tile loop runs in pairs, so every access names its
+// buffer at compile time; one barrier per tile.
 
 struct FwdTileBuf64 {
-  __attribute__((aligned(16))) uint16_t k[3][TILE * 64];    // K rows of the two heads, head 0's
-  __attribute__((aligned(16))) uint16_t vt[2][TILE * 64];   // V^T of the two heads
+  __attribute__((aligned(16))) uint16_t k[2][TILE * 64];    // K rows of the two heads
+  __attribute__((aligned(16))) uint16_t vt[2][TILE * 64];   // their V^T
+};
+struct FwdSelBuf64 {
+  __attribute__((aligned(16))) uint16_t k0[TILE * 64];      // head 0's K rows
   __attribute__((aligned(16))) float c[NWAVES][64];         // per wavefront: the carry of each key
 };
 
@@ -1153,7 +1161,8 @@ __global__ __launch_bounds__(NTHREADS, 2) void fwd64_kernel(
   using elem = uint16_t;
   using frag = OP::frag;
   constexpr int D = 64, G = 2, NS = 4, DB = 2, AS = 2;
-  __shared__ FwdTileBuf64 sB0, sB1;
+  __shared__ FwdTileBuf64 sB0, sB1;   // tile t's K rows and V^T in buffer t mod 2
+  __shared__ FwdSelBuf64 sS0, sS1;    // tile t's head-0 K rows and carry rows in buffer t mod 2
   constexpr int LDF = TILE + 4;
   __shared__ __attribute__((aligned(16))) float sF[NWAVES][TILE * LDF];   // each wavefront's F tile
 
@@ -1234,128 +1243,143 @@ __global__ __launch_bounds__(NTHREADS, 2) void fwd64_kernel(
   const RowsLane rl_k(k_ld, lane);
   const int cl = cols_lane(ldv, lane);
 
-  // everything key tile kt needs, into buffer B, by direct loads only (see bwd_kv64_kernel)
+  // key tile kt's K rows and V^T (into B), and its head-0 K rows and carry rows (into S), by direct
+  // loads only
   auto load_tile = [&](int kt, FwdTileBuf64& B) {
     const int kbase = kt * TILE;
     g2l_rows64(B.k[0], rs_k0, rl_k, k_ld, kbase, wave);
     g2l_rows64(B.k[1], rs_k1, rl_k, k_ld, kbase, wave);
-    if (!has_h0) g2l_rows64(B.k[2], rs_kh, rl_k, k_ld, kbase, wave);
     g2l_cols32(B.vt[0], rs_v0, cl, (int)ldv, kbase, wave);
     g2l_cols32(B.vt[1], rs_v1, cl, (int)ldv, kbase, wave);
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(rs_c, (lds_void_ptr)B.c[wave], 4, (kbase + n) * 4, 0, 0, 0);
+  };
+  auto load_sel = [&](int kt, FwdSelBuf64& S) {
+    const int kbase = kt * TILE;
+    g2l_rows64(S.k0, rs_kh, rl_k, k_ld, kbase, wave);
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(rs_c, (lds_void_ptr)S.c[wave], 4, (kbase + n) * 4, 0, 0, 0);
   };
   auto rfrag = [&](const elem* tile, int s) -> frag {
     return *reinterpret_cast<const frag*>(tile + swz64(n, 2 * s + h));
   };
 
+  // Key tile kt's selection: head 0's logits as (queries x keys), lane = key, so the running sum over
+  // queries stays within the lane; -F (logit units) = -(the carry at the block's first query + the
+  // selection by the block's earlier queries) goes to this wavefront's LDS rows, where the tile's
+  // softmax reads it in the (keys x queries) layout.
+  auto select = [&](int kt, const FwdSelBuf64& S) {
+    const int kbase = kt * TILE;
+    f32x16 l0t = zero16();
+#pragma unroll
+    for (int s = 0; s < NS; ++s) l0t = OP::mma(has_h0 ? qf[0][s] : q0f[s], rfrag(S.k0, s), l0t);
+    f32x16 sel;
+    // -relu as one v_med3 (see fwd_kernel)
+#pragma unroll
+    for (int i = 0; i < 16; ++i) sel[i] = __builtin_amdgcn_fmed3f(-l0t[i], -3.0e38f, 0.f);
+    const bool edge = (kbase + TILE - 1 >= q_off + rb * TILE) || (kbase + TILE > Tk) || kbase < exempt;
+    if (edge) {
+      // pairs exempt <= j < r; keys past the end and queries past the end hold zero rows
+      const int jk = kbase + n;
+      const int thr = jk >= exempt ? jk - (q_off + rb * TILE) - 4 * h : 32;
+#pragma unroll
+      for (int i = 0; i < 16; ++i) sel[i] = crow(i, 0) > thr ? sel[i] : 0.f;
+    }
+    float run = S.c[wave][n] * neg_inv_scale;
+    float* fw = sF[wave];
+#pragma unroll
+    for (int a = 0; a < 4; ++a) {
+      const Halves g = halves(((sel[4 * a] + sel[4 * a + 1]) + sel[4 * a + 2]) + sel[4 * a + 3]);
+      float p = (h == 0) ? run : run + g.lo;
+#pragma unroll
+      for (int t2 = 0; t2 < 4; ++t2) {
+        fw[crow(4 * a + t2, h) * LDF + n] = p;
+        p += sel[4 * a + t2];
+      }
+      run = (run + g.lo) + g.hi;
+    }
+  };
+
+  // the first tile's operands, head-0 rows and carry of the first two, and the first tile's F
   load_tile(wg_end - 1, sB0);
+  load_sel(wg_end - 1, sS0);
+  if (wg_end >= 2) load_sel(wg_end - 2, sS1);
   wait_loads();
   __syncthreads();
+  if (wg_end - 1 < my_end) select(wg_end - 1, sS0);
 
-  // one key tile (buffer t mod 2, named by ODD); INTERIOR and DAMP as in fwd_kernel
+  // tile t (buffer t mod 2, named by ODD); INTERIOR and DAMP as in fwd_kernel (INTERIOR for tile t;
+  // the selection of tile t + 1 checks its own tile)
   auto tile_step = [&](int t, auto interior_tag, auto damp_tag, auto odd_tag) __attribute__((always_inline)) {
     constexpr bool INTERIOR = decltype(interior_tag)::value;
     constexpr bool DAMP = decltype(damp_tag)::value;
     constexpr bool ODD = decltype(odd_tag)::value;
     FwdTileBuf64& B = ODD ? sB1 : sB0;
     const int kt = wg_end - 1 - t;
-    if (t + 1 < wg_end) load_tile(kt - 1, ODD ? sB0 : sB1);   // free since the last barrier
+    // free since the last barrier: the other tile buffer, and this parity's head-0 buffer (tile t's
+    // rows were used by the selection of tile t during tile t - 1)
+    if (t + 1 < wg_end) load_tile(kt - 1, ODD ? sB0 : sB1);
+    if (t + 2 < wg_end) load_sel(kt - 2, ODD ? sS1 : sS0);
     if (kt < my_end) {   // (a wavefront past the last query block has none)
       const int kbase = kt * TILE;
       const bool edge =
           !INTERIOR && ((kbase + TILE - 1 >= q_off + rb * TILE) || (kbase + TILE > Tk) || kbase < exempt);
-      auto body = [&]() {
-        // head 0's logits as (queries x keys), lane = key; -F through this wavefront's LDS rows
-        f32x16 l0t = zero16();
-        {
-          const elem* k0s = has_h0 ? B.k[0] : B.k[2];
+      f32x16 fs;   // -F of this tile, written by its selection
 #pragma unroll
-          for (int s = 0; s < NS; ++s) l0t = OP::mma(has_h0 ? qf[0][s] : q0f[s], rfrag(k0s, s), l0t);
+      for (int a = 0; a < 4; ++a) {
+        const float4 f4 = *reinterpret_cast<const float4*>(&sF[wave][n * LDF + 8 * a + 4 * h]);
+        fs[4 * a] = f4.x;
+        fs[4 * a + 1] = f4.y;
+        fs[4 * a + 2] = f4.z;
+        fs[4 * a + 3] = f4.w;
+      }
+      if constexpr (DAMP) {
+#pragma unroll
+        for (int i = 0; i < 16; ++i) fs[i] *= damp;
+      }
+#pragma unroll
+      for (int g = 0; g < G; ++g) {
+        f32x16 lg = fs;   // the product accumulates onto -F: lg = q.k - F/s
+#pragma unroll
+        for (int s = 0; s < NS; ++s) lg = OP::mma(rfrag(B.k[g], s), qf[g][s], lg);
+        if (edge) {
+          const int thr = min(q_abs, Tk - 1) - kbase - 4 * h;
+#pragma unroll
+          for (int i = 0; i < 16; ++i) lg[i] = crow(i, 0) <= thr ? lg[i] : -INFINITY;
         }
-        {
-          f32x16 sel;
+        float zmax = -INFINITY;
 #pragma unroll
-          for (int i = 0; i < 16; ++i) sel[i] = __builtin_amdgcn_fmed3f(-l0t[i], -3.0e38f, 0.f);
-          if (edge) {
-            const int jk = kbase + n;
-            const int thr = jk >= exempt ? jk - (q_off + rb * TILE) - 4 * h : 32;
-#pragma unroll
-            for (int i = 0; i < 16; ++i) sel[i] = crow(i, 0) > thr ? sel[i] : 0.f;
-          }
-          float run = B.c[wave][n] * neg_inv_scale;
-          float* fw = sF[wave];
-#pragma unroll
-          for (int a = 0; a < 4; ++a) {
-            const Halves g = halves(((sel[4 * a] + sel[4 * a + 1]) + sel[4 * a + 2]) + sel[4 * a + 3]);
-            float p = (h == 0) ? run : run + g.lo;
-#pragma unroll
-            for (int t2 = 0; t2 < 4; ++t2) {
-              fw[crow(4 * a + t2, h) * LDF + n] = p;
-              p += sel[4 * a + t2];
-            }
-            run = (run + g.lo) + g.hi;
-          }
-        }
-        lds_wave_sync();
-        f32x16 fs;
-#pragma unroll
-        for (int a = 0; a < 4; ++a) {
-          const float4 f4 = *reinterpret_cast<const float4*>(&sF[wave][n * LDF + 8 * a + 4 * h]);
-          fs[4 * a] = f4.x;
-          fs[4 * a + 1] = f4.y;
-          fs[4 * a + 2] = f4.z;
-          fs[4 * a + 3] = f4.w;
-        }
-        if constexpr (DAMP) {
-#pragma unroll
-          for (int i = 0; i < 16; ++i) fs[i] *= damp;
-        }
-#pragma unroll
-        for (int g = 0; g < G; ++g) {
-          f32x16 lg = fs;   // the product accumulates onto -F: lg = q.k - F/s
-#pragma unroll
-          for (int s = 0; s < NS; ++s) lg = OP::mma(rfrag(B.k[g], s), qf[g][s], lg);
-          if (edge) {
-            const int thr = min(q_abs, Tk - 1) - kbase - 4 * h;
-#pragma unroll
-            for (int i = 0; i < 16; ++i) lg[i] = crow(i, 0) <= thr ? lg[i] : -INFINITY;
-          }
-          float zmax = -INFINITY;
-#pragma unroll
-          for (int i = 0; i < 16; ++i) zmax = fmaxf(zmax, lg[i]);
-          const Halves zh = halves(zmax);
-          const float m_new = fmaxf(m[g], fmaxf(zh.lo, zh.hi) * sl2);
-          if (__any(m_new > m[g])) {
-            const float alpha = (m_new == -INFINITY) ? 1.f : fast_exp2(m[g] - m_new);
-            m[g] = m_new;
-            l[g] *= alpha;
-#pragma unroll
-            for (int db = 0; db < DB; ++db)
-#pragma unroll
-              for (int i = 0; i < 16; ++i) o[g][db][i] *= alpha;
-          }
-          const float mu = (m[g] == -INFINITY) ? 0.f : m[g];
-          float psum = 0.f;
-#pragma unroll
-          for (int i = 0; i < 16; ++i) {
-            const float p = fast_exp2(fmaf(lg[i], sl2, -mu));
-            lg[i] = p;
-            psum += p;
-          }
-          l[g] += psum;
-          frag pf[AS];
-#pragma unroll
-          for (int s = 0; s < AS; ++s) pf[s] = OP::from_acc(lg, s);
+        for (int i = 0; i < 16; ++i) zmax = fmaxf(zmax, lg[i]);
+        const Halves zh = halves(zmax);
+        const float m_new = fmaxf(m[g], fmaxf(zh.lo, zh.hi) * sl2);
+        if (__any(m_new > m[g])) {
+          const float alpha = (m_new == -INFINITY) ? 1.f : fast_exp2(m[g] - m_new);
+          m[g] = m_new;
+          l[g] *= alpha;
 #pragma unroll
           for (int db = 0; db < DB; ++db)
 #pragma unroll
-            for (int s = 0; s < AS; ++s)
-              o[g][db] = OP::mma(*reinterpret_cast<const frag*>(B.vt[g] + swz32(db * 32 + n, 2 * s + h)), pf[s],
-                                 o[g][db]);
+            for (int i = 0; i < 16; ++i) o[g][db][i] *= alpha;
         }
-      };
-      body();
+        const float mu = (m[g] == -INFINITY) ? 0.f : m[g];
+        float psum = 0.f;
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+          const float p = fast_exp2(fmaf(lg[i], sl2, -mu));
+          lg[i] = p;
+          psum += p;
+        }
+        l[g] += psum;
+        frag pf[AS];
+#pragma unroll
+        for (int s = 0; s < AS; ++s) pf[s] = OP::from_acc(lg, s);
+#pragma unroll
+        for (int db = 0; db < DB; ++db)
+#pragma unroll
+          for (int s = 0; s < AS; ++s)
+            o[g][db] = OP::mma(*reinterpret_cast<const frag*>(B.vt[g] + swz32(db * 32 + n, 2 * s + h)), pf[s],
+                               o[g][db]);
+      }
     }
+    // the next tile's F (after this tile's reads of the wavefront's F rows, in program order)
+    if (t + 1 < wg_end && kt - 1 < my_end) select(kt - 1, ODD ? sS0 : sS1);
     wait_loads();
     __syncthreads();   // the next tile's operands are in; every wavefront is done with this one
   };
