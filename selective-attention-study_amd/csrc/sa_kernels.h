@@ -1131,28 +1131,32 @@ __global__ __launch_bounds__(NTHREADS, (fwd_min_blocks<OP, D, G>())) void fwd_ke
 }
 
 // ---------------------------------------------------------------------------------------------
-// Forward, bf16 storage at head dim 64 with two heads per wavefront (the default there): fwd_kernel's
-// tile work with every key tile's operands loaded straight into LDS ahead of use (see
-// bwd_kv64_kernel), and the selection one tile ahead of the softmax: while tile t's logit products,
-// softmax and value products run, the wavefront also takes head 0's logits of tile t + 1 and turns
-// them into that tile's F (through its LDS rows, read at the start of tile t + 1), so each tile is
-// one block of independent products and arithmetic the compiler interleaves, with no wait inside it
-// for the F round trip. The K rows of the two heads and their V^T (swz64 / swz32) load one tile ahead
-// into two buffers; head 0's K rows and each wavefront's carry row two tiles ahead into two more;
-// all four are separate LDS variables and the tile loop runs in pairs, so every access names its
-// buffer at compile time; one barrier per tile.
+// Forward, bf16 storage at head dim 64 with G = 2 heads per wavefront (the default there) or one
+// (odd head counts, the per-head mode): fwd_kernel's tile work with every key tile's operands loaded
+// straight into LDS ahead of use (see bwd_kv64_kernel), and the selection one tile ahead of the
+// softmax: while tile t's logit products, softmax and value products run, the wavefront also takes
+// head 0's logits of tile t + 1 and turns them into that tile's F (through its LDS rows, read at the
+// start of tile t + 1), so each tile is one block of independent products and arithmetic the
+// compiler interleaves, with no wait inside it for the F round trip. A one-head group holding head 0
+// sends that head's whole adjusted logits through the LDS rows instead (as fwd_kernel does), so it
+// takes one logit product per tile. The K rows of the group's heads and their V^T (swz64 / swz32)
+// load one tile ahead into two buffers; head 0's K rows and each wavefront's carry row two tiles
+// ahead into two more; all four are separate LDS variables and the tile loop runs in pairs, so every
+// access names its buffer at compile time; one barrier per tile. Two workgroups per CU at G = 2,
+// three at G = 1.
 
+template <int G>
 struct FwdTileBuf64 {
-  __attribute__((aligned(16))) uint16_t k[2][TILE * 64];    // K rows of the two heads
-  __attribute__((aligned(16))) uint16_t vt[2][TILE * 64];   // their V^T
+  __attribute__((aligned(16))) uint16_t k[G][TILE * 64];    // K rows of the group's heads
+  __attribute__((aligned(16))) uint16_t vt[G][TILE * 64];   // their V^T
 };
 struct FwdSelBuf64 {
   __attribute__((aligned(16))) uint16_t k0[TILE * 64];      // head 0's K rows
   __attribute__((aligned(16))) float c[NWAVES][64];         // per wavefront: the carry of each key
 };
 
-template <bool CV>   // CV: as fwd_kernel
-__global__ __launch_bounds__(NTHREADS, 2) void fwd64_kernel(
+template <bool CV, int G>   // CV: as fwd_kernel; G: heads per wavefront (1 or 2)
+__global__ __launch_bounds__(NTHREADS, G == 1 ? 3 : 2) void fwd64_kernel(
     const uint16_t* __restrict__ q, const uint16_t* __restrict__ k, const uint16_t* __restrict__ vt,
     const float* __restrict__ carry, float* __restrict__ out, float* __restrict__ rmax, float* __restrict__ rden,
     uint16_t* __restrict__ y, Strides ys, int H, int Tq, int Tk, Strides qs, Strides ks, int q_off, int64_t ldv,
@@ -1160,11 +1164,13 @@ __global__ __launch_bounds__(NTHREADS, 2) void fwd64_kernel(
   using OP = OpBF16;
   using elem = uint16_t;
   using frag = OP::frag;
-  constexpr int D = 64, G = 2, NS = 4, DB = 2, AS = 2;
-  __shared__ FwdTileBuf64 sB0, sB1;   // tile t's K rows and V^T in buffer t mod 2
+  constexpr int D = 64, NS = 4, DB = 2, AS = 2;
+  static_assert(G == 1 || G == 2, "one or two heads per wavefront");
+  __shared__ FwdTileBuf64<G> sB0, sB1;   // tile t's K rows and V^T in buffer t mod 2
   __shared__ FwdSelBuf64 sS0, sS1;    // tile t's head-0 K rows and carry rows in buffer t mod 2
   constexpr int LDF = TILE + 4;
   __shared__ __attribute__((aligned(16))) float sF[NWAVES][TILE * LDF];   // each wavefront's F tile
+  __shared__ __attribute__((aligned(16))) float sDamp[NWAVES][TILE];      // its queries' damping factors
 
   const int tid = threadIdx.x, lane = tid & 63, wave = wave_id();
   const int n = lane & 31, h = lane >> 5;
@@ -1173,6 +1179,7 @@ __global__ __launch_bounds__(NTHREADS, 2) void fwd64_kernel(
   const int b = bxy.y / groups, gi = bxy.y % groups;
   const int hd0 = gi * G;
   const bool has_h0 = (gi == 0);
+  const bool whole = G == 1 && has_h0;   // head 0's adjusted logits come through LDS whole
   const int NBq = (Tq + TILE - 1) / TILE;
   const int NKT = (Tk + TILE - 1) / TILE;
   const int qsb = gridDim.x - 1 - bxy.x;
@@ -1230,13 +1237,14 @@ __global__ __launch_bounds__(NTHREADS, 2) void fwd64_kernel(
     damp = fminf(1.f, train_len / (float)(q_abs + 1));
     if (damp_mode == 2) damp = sqrtf(damp);
   }
+  if (lane < TILE) sDamp[wave][lane] = damp;   // (read after the first barrier)
 
   // key-side sources and this lane's parts of the direct loads
   const __amdgpu_buffer_rsrc_t rs_k0 = rsrc(k_head(hd0), (int64_t)Tk * k_ld * 2);
-  const __amdgpu_buffer_rsrc_t rs_k1 = rsrc(k_head(hd0 + 1), (int64_t)Tk * k_ld * 2);
+  const __amdgpu_buffer_rsrc_t rs_k1 = rsrc(k_head(hd0 + G - 1), (int64_t)Tk * k_ld * 2);
   const __amdgpu_buffer_rsrc_t rs_kh = rsrc(k_head(0), (int64_t)Tk * k_ld * 2);
   const __amdgpu_buffer_rsrc_t rs_v0 = rsrc(vt + (seq_row + hd0) * D * ldv, (int64_t)D * ldv * 2);
-  const __amdgpu_buffer_rsrc_t rs_v1 = rsrc(vt + (seq_row + hd0 + 1) * D * ldv, (int64_t)D * ldv * 2);
+  const __amdgpu_buffer_rsrc_t rs_v1 = rsrc(vt + (seq_row + hd0 + G - 1) * D * ldv, (int64_t)D * ldv * 2);
   // this wavefront's carry row (its query block's; keys past the end read zero)
   const __amdgpu_buffer_rsrc_t rs_c =
       rsrc(carry + ((int64_t)b * NBq + min(rb, NBq - 1)) * Tk, (int64_t)Tk * 4);
@@ -1245,12 +1253,14 @@ __global__ __launch_bounds__(NTHREADS, 2) void fwd64_kernel(
 
   // key tile kt's K rows and V^T (into B), and its head-0 K rows and carry rows (into S), by direct
   // loads only
-  auto load_tile = [&](int kt, FwdTileBuf64& B) {
+  auto load_tile = [&](int kt, FwdTileBuf64<G>& B) {
     const int kbase = kt * TILE;
     g2l_rows64(B.k[0], rs_k0, rl_k, k_ld, kbase, wave);
-    g2l_rows64(B.k[1], rs_k1, rl_k, k_ld, kbase, wave);
     g2l_cols32(B.vt[0], rs_v0, cl, (int)ldv, kbase, wave);
-    g2l_cols32(B.vt[1], rs_v1, cl, (int)ldv, kbase, wave);
+    if constexpr (G == 2) {
+      g2l_rows64(B.k[1], rs_k1, rl_k, k_ld, kbase, wave);
+      g2l_cols32(B.vt[1], rs_v1, cl, (int)ldv, kbase, wave);
+    }
   };
   auto load_sel = [&](int kt, FwdSelBuf64& S) {
     const int kbase = kt * TILE;
@@ -1264,8 +1274,9 @@ __global__ __launch_bounds__(NTHREADS, 2) void fwd64_kernel(
   // Key tile kt's selection: head 0's logits as (queries x keys), lane = key, so the running sum over
   // queries stays within the lane; -F (logit units) = -(the carry at the block's first query + the
   // selection by the block's earlier queries) goes to this wavefront's LDS rows, where the tile's
-  // softmax reads it in the (keys x queries) layout.
-  auto select = [&](int kt, const FwdSelBuf64& S) {
+  // softmax reads it in the (keys x queries) layout (with `whole`: q.k - damp F/s, damping per row).
+  auto select = [&](int kt, const FwdSelBuf64& S, auto damp_tag) {
+    constexpr bool DAMP = decltype(damp_tag)::value;
     const int kbase = kt * TILE;
     f32x16 l0t = zero16();
 #pragma unroll
@@ -1288,22 +1299,26 @@ __global__ __launch_bounds__(NTHREADS, 2) void fwd64_kernel(
     for (int a = 0; a < 4; ++a) {
       const Halves g = halves(((sel[4 * a] + sel[4 * a + 1]) + sel[4 * a + 2]) + sel[4 * a + 3]);
       float p = (h == 0) ? run : run + g.lo;
+      float4 dm = make_float4(1.f, 1.f, 1.f, 1.f);   // the rows' damping factors
+      if constexpr (DAMP && G == 1) dm = *reinterpret_cast<const float4*>(&sDamp[wave][8 * a + 4 * h]);
+      const float dmv[4] = {dm.x, dm.y, dm.z, dm.w};
 #pragma unroll
       for (int t2 = 0; t2 < 4; ++t2) {
-        fw[crow(4 * a + t2, h) * LDF + n] = p;
+        float f = p;
+        if (whole) f = DAMP ? fmaf(dmv[t2], p, l0t[4 * a + t2]) : p + l0t[4 * a + t2];
+        fw[crow(4 * a + t2, h) * LDF + n] = f;
         p += sel[4 * a + t2];
       }
       run = (run + g.lo) + g.hi;
     }
   };
 
-  // the first tile's operands, head-0 rows and carry of the first two, and the first tile's F
+  // the first tile's operands, head-0 rows and carry of the first two (its F at the sweep's start)
   load_tile(wg_end - 1, sB0);
   load_sel(wg_end - 1, sS0);
   if (wg_end >= 2) load_sel(wg_end - 2, sS1);
   wait_loads();
   __syncthreads();
-  if (wg_end - 1 < my_end) select(wg_end - 1, sS0);
 
   // tile t (buffer t mod 2, named by ODD); INTERIOR and DAMP as in fwd_kernel (INTERIOR for tile t;
   // the selection of tile t + 1 checks its own tile)
@@ -1311,7 +1326,7 @@ __global__ __launch_bounds__(NTHREADS, 2) void fwd64_kernel(
     constexpr bool INTERIOR = decltype(interior_tag)::value;
     constexpr bool DAMP = decltype(damp_tag)::value;
     constexpr bool ODD = decltype(odd_tag)::value;
-    FwdTileBuf64& B = ODD ? sB1 : sB0;
+    FwdTileBuf64<G>& B = ODD ? sB1 : sB0;
     const int kt = wg_end - 1 - t;
     // free since the last barrier: the other tile buffer, and this parity's head-0 buffer (tile t's
     // rows were used by the selection of tile t during tile t - 1)
@@ -1331,14 +1346,18 @@ __global__ __launch_bounds__(NTHREADS, 2) void fwd64_kernel(
         fs[4 * a + 3] = f4.w;
       }
       if constexpr (DAMP) {
+        if (!whole) {
 #pragma unroll
-        for (int i = 0; i < 16; ++i) fs[i] *= damp;
+          for (int i = 0; i < 16; ++i) fs[i] *= damp;
+        }
       }
 #pragma unroll
       for (int g = 0; g < G; ++g) {
         f32x16 lg = fs;   // the product accumulates onto -F: lg = q.k - F/s
+        if (!whole) {
 #pragma unroll
-        for (int s = 0; s < NS; ++s) lg = OP::mma(rfrag(B.k[g], s), qf[g][s], lg);
+          for (int s = 0; s < NS; ++s) lg = OP::mma(rfrag(B.k[g], s), qf[g][s], lg);
+        }
         if (edge) {
           const int thr = min(q_abs, Tk - 1) - kbase - 4 * h;
 #pragma unroll
@@ -1379,13 +1398,14 @@ __global__ __launch_bounds__(NTHREADS, 2) void fwd64_kernel(
       }
     }
     // the next tile's F (after this tile's reads of the wavefront's F rows, in program order)
-    if (t + 1 < wg_end && kt - 1 < my_end) select(kt - 1, ODD ? sS0 : sS1);
+    if (t + 1 < wg_end && kt - 1 < my_end) select(kt - 1, ODD ? sS0 : sS1, damp_tag);
     wait_loads();
     __syncthreads();   // the next tile's operands are in; every wavefront is done with this one
   };
   const int i_lo = min((exempt + TILE - 1) / TILE, wg_end);
   const int i_hi = max(i_lo, min(min(q_off + qsb * NWAVES * TILE, Tk) / TILE, wg_end));
   auto sweep = [&](auto damp_tag) {
+    if (wg_end - 1 < my_end) select(wg_end - 1, sS0, damp_tag);   // the first tile's F
     auto run = [&](int t0, int t1, auto interior_tag) {
       int t = t0;
       if (t < t1 && (t & 1)) tile_step(t++, interior_tag, damp_tag, std::true_type{});
@@ -3274,23 +3294,23 @@ void launch_fwd(const FwdCall& c, const typename OP::elem* vt, int64_t ldv) {
   const bool cv = c.qs.row == D && c.qs.head == (int64_t)c.Tq * D && c.qs.seq == (int64_t)c.H * c.qs.head &&
                   c.ks.row == D && c.ks.seq == (int64_t)c.H * c.ks.head;
   TimedLaunch timed(SA_KERNEL_FORWARD, c.st);
-  if constexpr (sizeof(elem) == 2 && D == 64 && G == 2) {   // the direct-load kernel
+  if constexpr (sizeof(elem) == 2 && D == 64 && G <= 2) {   // the direct-load kernel
 #define SA_LAUNCH_FWD64(CVV)                                                                                      \
-  hipLaunchKernelGGL((fwd64_kernel<CVV>), grid, dim3(NTHREADS), 0, c.st, static_cast<const elem*>(c.q),          \
+  hipLaunchKernelGGL((fwd64_kernel<CVV, G>), grid, dim3(NTHREADS), 0, c.st, static_cast<const elem*>(c.q),       \
                      static_cast<const elem*>(c.k), vt, c.carry, c.out, c.rmax, c.rden, static_cast<elem*>(c.y),  \
                      c.ys, c.H, c.Tq, c.Tk, c.qs, c.ks, c.q_off, ldv, c.exempt, c.scale, c.damp_mode, c.train_len)
     if (cv) SA_LAUNCH_FWD64(true);
     else SA_LAUNCH_FWD64(false);
 #undef SA_LAUNCH_FWD64
-    return;
-  }
+  } else {
 #define SA_LAUNCH_FWD(CVV)                                                                                        \
   hipLaunchKernelGGL((fwd_kernel<OP, D, G, CVV>), grid, dim3(NTHREADS), 0, c.st, static_cast<const elem*>(c.q),  \
                      static_cast<const elem*>(c.k), vt, c.carry, c.out, c.rmax, c.rden, static_cast<elem*>(c.y),  \
                      c.ys, c.H, c.Tq, c.Tk, c.qs, c.ks, c.q_off, ldv, c.exempt, c.scale, c.damp_mode, c.train_len)
-  if (cv) SA_LAUNCH_FWD(true);
-  else SA_LAUNCH_FWD(false);
+    if (cv) SA_LAUNCH_FWD(true);
+    else SA_LAUNCH_FWD(false);
 #undef SA_LAUNCH_FWD
+  }
 }
 
 template <class OP, int D>
@@ -3301,7 +3321,7 @@ int forward_impl(const FwdCall& c) {
   const int dtype = sizeof(elem) == 2 ? SA_DTYPE_BF16 : SA_DTYPE_F32;
   const int G = auto_group(dtype, D, c.H, c.group, false);
   // V^T in the column order of fwd64_kernel's direct loads when it runs
-  const bool crow = sizeof(elem) == 2 && D == 64 && G == 2;
+  const bool crow = sizeof(elem) == 2 && D == 64 && G <= 2;
   launch_transpose<elem, D>(static_cast<const elem*>(c.v), vt, c.Tk, ldv, c.vs, c.H, (int64_t)c.nseq * c.H, c.st,
                             crow);
   int rc = run_selection<OP, D>(c, c.st);

@@ -4,7 +4,8 @@ bf16-valued inputs (reference tests/test_selective_kernels.py:141-172, 203-242).
 The launch policy picks the instance from (head_dim, heads, group, bwd_group); with H = 4:
 
     forward   head_dim 16 / 32 (run at 32): group 1 -> 1 head per wavefront, 2 -> 2, 4 / None -> 4
-              head_dim 64:                  group 1 -> 1, 2 / None -> 2, 4 -> 4
+              head_dim 64:                  group 1 -> 1, 2 / None -> 2, 4 -> 4 (an odd head count
+                                            runs 1: the prefill cases at H = 3 and H = 1)
               head_dim 128:                 1
     backward  head_dim 16 / 32: bwd_group 2 -> 2 heads per wavefront (key side and query side),
               1 / None -> 1;  head_dim 64, 128: 1
@@ -82,7 +83,7 @@ def test_bf16_exempt_matches_oracle(cuda, head_dim, heads, exempt):
 
 
 @pytest.mark.parametrize("damp", ["linear", "sqrt"])
-@pytest.mark.parametrize("head_dim,group", [(32, 4), (32, 2), (64, None), (128, None)])
+@pytest.mark.parametrize("head_dim,group", [(32, 4), (32, 2), (64, None), (64, 1), (128, None)])
 def test_bf16_history_damping(cuda, damp, head_dim, group):
     """Evaluation-only history damping on the bf16 forward instances (reference
     tests/test_selective_kernels.py:223-242): damping with train_len >= T changes nothing, and with
@@ -108,7 +109,8 @@ def test_bf16_history_damping(cuda, damp, head_dim, group):
     assert (got - plain).abs().max().item() > 0.1
 
 
-@pytest.mark.parametrize("head_dim,heads,chunk", [(64, 4, 256), (32, 4, 100), (128, 2, 333)])
+@pytest.mark.parametrize("head_dim,heads,chunk", [(64, 4, 256), (64, 3, 300), (64, 1, 192), (32, 4, 100),
+                                                  (128, 2, 333)])
 def test_bf16_chunked_prefill_matches_oracle(cuda, head_dim, heads, chunk):
     """Chunked prefill on the bf16 instances against the oracle (output and carried state), and
     against the single-shot bf16 forward."""
