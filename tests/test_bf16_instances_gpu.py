@@ -154,3 +154,19 @@ def test_bf16_packed_projection_matches_oracle(cuda, head_dim, heads):
     for i, name in enumerate(("dq", "dk", "dv")):
         rel = ((got[:, :, i] - want[:, :, i]).norm() / want[:, :, i].norm()).item()
         assert rel < 3e-2, (name, rel)
+
+
+@pytest.mark.parametrize("seq", [1, 2, 31, 32, 33, 64, 65, 97, 160])
+@pytest.mark.parametrize("heads", [1, 2, 3])
+def test_bf16_head_dim_64_forward_short_sequences(cuda, seq, heads):
+    """The direct-load forward at head dim 64 (two heads per wavefront at H = 2, one at H = 1, 3) on
+    sequences of one to five key tiles: its selection runs one tile ahead and its loads two, so the
+    first and last tiles of a workgroup take the loop's edge cases."""
+    print(f"case bf16 D=64 short seq={seq} heads={heads}", flush=True)
+    q, k, v, _ = _inputs(2, heads, seq, 64, seed=seq + 7 * heads, scale=1.3)
+    got, aux = kernels.selective_attention_forward(q.to(cuda), k.to(cuda), v.to(cuda), return_aux=True)
+    want = sa_oracle.attention(q.double(), k.double(), v.double())
+    assert (got.cpu().double() - want).abs().max().item() < 3e-2
+    total = sa_oracle.selection_totals(q.double(), k.double())
+    err = (aux["selected_total"].cpu().double() - total).abs().max().item()
+    assert err <= 1e-4 * max(total.abs().max().item(), 1.0), err
