@@ -12,8 +12,8 @@ namespace sa_host {
 int launch_bwd_kv_bf16(int D, int G, bool cv, const KvLaunch& a) {
   if (D != 64) return launch_bwd_kv_bf16_generic(D, G, cv, a);
   if (a.H == 1) return launch_bwd_kv64_solo(cv, a);
-  if (cv) launch_kv64_from<true>(a);
-  else launch_kv64_from<false>(a);
+  if (cv) launch_kv64_from<true, false>(a);
+  else launch_kv64_from<false, false>(a);
   return launch_status();
 }
 

@@ -356,6 +356,15 @@ __device__ __forceinline__ int swz64(int r, int c) { return r * 64 + (((c + (r >
 // 64 four-byte banks) touches 16 distinct bank groups.
 __device__ __forceinline__ int swz32(int r, int c) { return r * 32 + ((c ^ ((r >> 2) & 3)) << 3); }
 
+// Unpadded LDS rows of 64 bf16 read both ways: by lane-per-row fragment reads and by transposing
+// reads (get_trq). Chunk c of row r is stored at chunk c ^ f(r), f(r) = 2 (r mod 4) ^ (r/4 mod 4).
+// A 16-byte read of one chunk by 16 consecutive rows (16 lanes per pass over 64 four-byte banks):
+// the eight rows of each parity take eight distinct chunks. A transposing read of four consecutive
+// rows, an aligned 32-byte column range of each (16 lanes per pass over 32 banks, or 32 lanes over
+// 64 banks reading 64 bytes of each row): f(r) / 2 takes four distinct values on the four rows, and
+// rows two apart differ in bit 2 of f, so every pass touches distinct banks.
+__device__ __forceinline__ int swzq(int r, int c) { return r * 64 + ((c ^ (((r & 3) << 1) ^ ((r >> 2) & 3))) << 3); }
+
 typedef __attribute__((address_space(3))) void* lds_void_ptr;
 
 // A buffer resource over `bytes` bytes from p (loads past them read zero).
@@ -389,6 +398,46 @@ __device__ __forceinline__ void g2l_rows64(uint16_t* tile, __amdgpu_buffer_rsrc_
                                            int row0, int m) {
   __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_void_ptr)(tile + 512 * m), 16, (m & 1) ? rl.v1 : rl.v0,
                                            (row0 + 8 * m) * ld * 2, 0, 0);
+}
+//   rowsq: a [32 rows][64] tile in swzq layout, as rows64. Slot 64m + l holds row r = 8m + l/8,
+//          stored chunk l mod 8, so logical chunk (l mod 8) ^ f(r), f(r) = 2 (l/8 mod 4) ^ (l/32)
+//          ^ 2 (m mod 2): c0 = (l mod 8) ^ 2 (l/8 mod 4) ^ l/32 for even m, c0 ^ 2 for odd m.
+struct RowsLaneQ {
+  int v0, v1;   // the lane's byte offsets for the even and the odd parts
+  __device__ __forceinline__ RowsLaneQ(int ld, int lane) {
+    const int c0 = (lane & 7) ^ (((lane >> 3) & 3) << 1) ^ (lane >> 5);
+    v0 = ((lane >> 3) * ld + 8 * c0) * 2;
+    v1 = ((lane >> 3) * ld + 8 * (c0 ^ 2)) * 2;
+  }
+};
+__device__ __forceinline__ void g2l_rowsq(uint16_t* tile, __amdgpu_buffer_rsrc_t rs, const RowsLaneQ& rl, int ld,
+                                          int row0, int m) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_void_ptr)(tile + 512 * m), 16, (m & 1) ? rl.v1 : rl.v0,
+                                           (row0 + 8 * m) * ld * 2, 0, 0);
+}
+// The A operand of K step s of a product over the rows of a [32 rows][64] swzq tile (Y^T X with Y
+// the tile and X a C-layout tile entering as the B operand, OpBF16::from_acc): lane l gets column
+// 32 db + l % 32 of the tile at the rows X's fragment holds, in the accumulator's row order:
+// element e is row crow(8s + e, l / 32) = 16s + 8(e / 4) + 4(l / 32) + e % 4. Two transposing
+// reads (e / 4 = 0, 1): lane i of a 16-lane group gets, as element t, element i % 4 of the 8 bytes
+// that lane 4t + i/4 of the group addresses, so lane k of the group addresses row base + k/4,
+// columns 4 (k mod 4) .. +3 of the group's 16 (measured lane layout, see get_tr).
+__device__ __forceinline__ bf16x8 get_trq(const uint16_t* t, int lane, int db, int s) {
+  const int g = lane >> 4, k = lane & 15;
+  const int c = 4 * db + 2 * (g & 1) + ((k & 3) >> 1);   // the 16-byte chunk of the lane's 4 columns
+  bf16x8 f;
+#pragma unroll
+  for (int hf = 0; hf < 2; ++hf) {
+    const int r = 16 * s + 8 * hf + 4 * (g >> 1) + (k >> 2);
+    typedef __attribute__((address_space(3))) short4v* lds_s4;
+    const short4v v = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s4)(t + swzq(r, c) + 4 * (k & 1)));
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const short x = v[e];
+      f[4 * hf + e] = *reinterpret_cast<const bf16_t*>(&x);
+    }
+  }
+  return f;
 }
 __device__ __forceinline__ void g2l_cols32(uint16_t* tile, __amdgpu_buffer_rsrc_t rs, int vl, int ld, int col0,
                                            int m) {
@@ -1454,7 +1503,8 @@ __global__ __launch_bounds__(NTHREADS, G == 1 ? 3 : 2) void fwd64_kernel(
 
 // ---------------------------------------------------------------------------------------------
 // Backward preparation: lse = rmax + log2(rden), ndbar = -rowsum(dO * O) (negated: the dO.v
-// products accumulate onto it), and the transposed copies Q^T, dO^T, K^T (R, D, ldt). The
+// products accumulate onto it), and the transposed copies K^T and (except at bf16 head dim 64,
+// whose key-side kernel reads its Q, dO rows transposed from LDS) Q^T, dO^T (R, D, ldt). The
 // statistics are laid out (R, ldt), each head's rows padded to ldt with lse = +inf (P = 0) and
 // ndbar = 0, so a 32-row tile of them is always in bounds; they take D/8 lanes per row (8 elements
 // each, so the loads of a row are contiguous across its lanes); transposes go by tiles.
@@ -1540,8 +1590,8 @@ __global__ __launch_bounds__(NTHREADS) void transpose_kernel(const E* __restrict
 // word joins the same half-word of two rows), eight 16-byte column stores. A wavefront's loads and
 // stores cover whole 128-byte segments (eight lanes per row or column).
 // CROW: each output row holds its 16-column blocks in C-layout row order (groups of four columns
-// 0, 2, 1, 3), the order in which a transposed operand tile enters the products of the key-side
-// backward kernel at head dim 64, so that its direct loads into LDS are plain copies.
+// 0, 2, 1, 3), the order in which a transposed operand tile enters the products of the forward
+// kernel at head dim 64 (V^T), so that its direct loads into LDS are plain copies.
 template <int D, bool CROW>
 __global__ __launch_bounds__(NTHREADS) void transpose8_kernel(const uint16_t* __restrict__ in,
                                                               uint16_t* __restrict__ outT, int T, int64_t ldt,
@@ -2108,27 +2158,28 @@ __global__ __launch_bounds__(NTHREADS, (kv_min_blocks<OP, D, G>())) void bwd_kv_
 // C2, C3, C4's model and C5): bwd_kv_kernel's tile work, with every query tile's operands loaded
 // straight from global memory into LDS one tile ahead -- no staging registers, no load latency at
 // the start of a tile, one barrier per tile -- into two buffers of unpadded, swizzled tiles: the Q
-// and dO rows (and head 0's Q rows) in swz64 layout, their transposed copies (which the transpose
-// writes in C-layout column order) in swz32 layout. The wavefront's own K rows sit in registers
-// beside head 0's, its V rows in LDS.
+// and dO rows (and head 0's Q rows) in swzq layout, read as rows by the logit products and
+// transposed (get_trq) by the dK, dV products, so no transposed copies are loaded. The wavefront's
+// own K rows sit in registers beside head 0's, its V rows in LDS.
 
-// One tile buffer of bwd_kv64_kernel: the Q, dO, head 0's Q rows (swz64), their transposed copies
-// (swz32), the rows' lse and -dbar (slots 32.. repeat rows 0..31), and per wavefront each lane's
-// carry at the tile's first query.
+// One tile buffer of bwd_kv64_kernel: the Q, dO and head 0's Q rows (swzq), the rows' lse and
+// -dbar (slots 32.. repeat rows 0..31), and per wavefront each lane's carry at the tile's first query.
 struct KvTileBuf64 {
   __attribute__((aligned(16))) uint16_t r[3][TILE * 64];
-  __attribute__((aligned(16))) uint16_t t[3][TILE * 64];
   __attribute__((aligned(16))) float stat[2][64];
   __attribute__((aligned(16))) float hist[NWAVES][64];
 };
 
-template <bool CV>   // CV: every view is the contiguous (nseq, H, T, D) layout of sa_backward
+// CV: every view is the contiguous (nseq, H, T, D) layout of sa_backward. SOLO: one-head sequences
+// only (every workgroup runs head 0's loop; the other heads' loop, with its registers for head 0's
+// K rows and dK share, is not built).
+template <bool CV, bool SOLO>
 __global__ __launch_bounds__(NTHREADS, 2) void bwd_kv64_kernel(
     const uint16_t* __restrict__ q, const uint16_t* __restrict__ k, const uint16_t* __restrict__ v,
-    const uint16_t* __restrict__ qt, const uint16_t* __restrict__ dout, const uint16_t* __restrict__ dot, Strides qs,
-    Strides ks, Strides vs, Strides dos, const float* __restrict__ lse, const float* __restrict__ dbar,
-    const float* __restrict__ carry, float* __restrict__ ucheck, float* __restrict__ dk0h, float* __restrict__ dk0x,
-    GradView dkv, GradView dvv, int nseq, int H, int T, int64_t ldt, int exempt, float scale) {
+    const uint16_t* __restrict__ dout, Strides qs, Strides ks, Strides vs, Strides dos,
+    const float* __restrict__ lse, const float* __restrict__ dbar, const float* __restrict__ carry,
+    float* __restrict__ ucheck, float* __restrict__ dk0h, float* __restrict__ dk0x, GradView dkv, GradView dvv,
+    int nseq, int H, int T, int64_t ldt, int exempt, float scale) {
   using OP = OpBF16;
   using elem = uint16_t;
   using frag = OP::frag;
@@ -2176,7 +2227,7 @@ __global__ __launch_bounds__(NTHREADS, 2) void bwd_kv64_kernel(
       const int r = c / (D / 8), cc = c % (D / 8);
       const bool ok = key0 + r < T;
       const uint4 v4 = *reinterpret_cast<const uint4*>(vh + (int64_t)(ok ? key0 + r : 0) * view_ld(vs) + cc * 8);
-      *reinterpret_cast<uint4*>(&sV[wave][swz64(r, cc)]) = ok ? v4 : make_uint4(0u, 0u, 0u, 0u);
+      *reinterpret_cast<uint4*>(&sV[wave][swzq(r, cc)]) = ok ? v4 : make_uint4(0u, 0u, 0u, 0u);
     }
   }
 
@@ -2200,13 +2251,9 @@ __global__ __launch_bounds__(NTHREADS, 2) void bwd_kv64_kernel(
   const __amdgpu_buffer_rsrc_t rs_q = rsrc(view_head(q, qs, hh), (int64_t)T * q_ld * 2);
   const __amdgpu_buffer_rsrc_t rs_do = rsrc(view_head(dout, dos, hh), (int64_t)T * do_ld * 2);
   const __amdgpu_buffer_rsrc_t rs_q0 = rsrc(view_head(q, qs, 0), (int64_t)T * q_ld * 2);
-  const __amdgpu_buffer_rsrc_t rs_qt = rsrc(qt + (seq_row + hh) * D * ldt, (int64_t)D * ldt * 2);
-  const __amdgpu_buffer_rsrc_t rs_dot = rsrc(dot + (seq_row + hh) * D * ldt, (int64_t)D * ldt * 2);
-  const __amdgpu_buffer_rsrc_t rs_q0t = rsrc(qt + seq_row * D * ldt, (int64_t)D * ldt * 2);
   const __amdgpu_buffer_rsrc_t rs_lse = rsrc(lse + (seq_row + hh) * ldt, ldt * 4);
   const __amdgpu_buffer_rsrc_t rs_ndb = rsrc(dbar + (seq_row + hh) * ldt, ldt * 4);
-  const RowsLane rl_q(q_ld, lane), rl_do(do_ld, lane);
-  const int cl = cols_lane(ldt, lane);
+  const RowsLaneQ rl_q(q_ld, lane), rl_do(do_ld, lane);
 
   // Everything query tile qb needs, into buffer B, by direct loads only (the tile loop holds no
   // register loads: the vector-memory counter drains in issue order, so waiting for one would wait
@@ -2221,44 +2268,37 @@ __global__ __launch_bounds__(NTHREADS, 2) void bwd_kv64_kernel(
       __builtin_amdgcn_raw_ptr_buffer_load_lds(rs_ndb, (lds_void_ptr)B.stat[1], 4, (lane & 31) * 4, qbase * 4, 0, 0);
     __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc(carry_b + (int64_t)qb * T, (int64_t)T * 4),
                                              (lds_void_ptr)B.hist[wave], 4, j * 4, 0, 0, 0);
-    g2l_rows64(B.r[0], rs_q, rl_q, q_ld, qbase, wave);
-    g2l_rows64(B.r[1], rs_do, rl_do, do_ld, qbase, wave);
-    g2l_cols32(B.t[0], rs_qt, cl, (int)ldt, qbase, wave);
-    g2l_cols32(B.t[1], rs_dot, cl, (int)ldt, qbase, wave);
-    if (!has_h0) {
-      g2l_rows64(B.r[2], rs_q0, rl_q, q_ld, qbase, wave);
-      g2l_cols32(B.t[2], rs_q0t, cl, (int)ldt, qbase, wave);
-    }
+    g2l_rowsq(B.r[0], rs_q, rl_q, q_ld, qbase, wave);
+    g2l_rowsq(B.r[1], rs_do, rl_do, do_ld, qbase, wave);
+    if (!has_h0) g2l_rowsq(B.r[2], rs_q0, rl_q, q_ld, qbase, wave);
   };
   // the first tile (NB - 1)
   load_tile(NB - 1, sB0);
   wait_loads();
   __syncthreads();
 
-  // acc[db] (D x keys) += Y^T X: Y a transposed tile (rows d, queries in C-layout order, swz32), X
-  // a C-layout (queries x keys) tile; with split, X also enters as its rounding residual.
-  auto acc_t = [&](f32x16 (&acc)[DB], const elem* yt, const f32x16& x, bool split) {
+  // acc[db] (D x keys) += Y^T X: Y a (queries x D) row tile (swzq, read transposed), X a C-layout
+  // (queries x keys) tile; with split, X also enters as its rounding residual.
+  auto acc_t = [&](f32x16 (&acc)[DB], const elem* y, const f32x16& x, bool split) {
     frag xf[AS];
 #pragma unroll
     for (int s = 0; s < AS; ++s) xf[s] = OP::from_acc(x, s);
 #pragma unroll
     for (int db = 0; db < DB; ++db)
 #pragma unroll
-      for (int s = 0; s < AS; ++s)
-        acc[db] = OP::mma(*reinterpret_cast<const frag*>(yt + swz32(db * 32 + n, 2 * s + h)), xf[s], acc[db]);
+      for (int s = 0; s < AS; ++s) acc[db] = OP::mma(get_trq(y, lane, db, s), xf[s], acc[db]);
     if (split) {
 #pragma unroll
       for (int s = 0; s < AS; ++s) xf[s] = OP::from_acc_lo(x, s);
 #pragma unroll
       for (int db = 0; db < DB; ++db)
 #pragma unroll
-        for (int s = 0; s < AS; ++s)
-          acc[db] = OP::mma(*reinterpret_cast<const frag*>(yt + swz32(db * 32 + n, 2 * s + h)), xf[s], acc[db]);
+        for (int s = 0; s < AS; ++s) acc[db] = OP::mma(get_trq(y, lane, db, s), xf[s], acc[db]);
     }
   };
-  // fragment s of row n of a swz64 tile (A operand: lane = query row; or B: lane = key)
+  // fragment s of row n of a swzq tile (A operand: lane = query row; or B: lane = key)
   auto rfrag = [&](const elem* tile, int s) -> frag {
-    return *reinterpret_cast<const frag*>(tile + swz64(n, 2 * s + h));
+    return *reinterpret_cast<const frag*>(tile + swzq(n, 2 * s + h));
   };
 
   // Keys below `exempt` are never selected, so they gather attention from every later query and
@@ -2306,16 +2346,16 @@ __global__ __launch_bounds__(NTHREADS, 2) void bwd_kv64_kernel(
           for (int s = 0; s < NS; ++s) dp = OP::mma(rfrag(B.r[1], s), rfrag(sV[wave], s), dp);
           f32x16 pr, dz;
           p_dz_tile<false>(lg, dp, B.stat[0], sl2, h, edge, mk, pr, dz);
-          acc_t(dvt, B.t[1], pr, split);
+          acc_t(dvt, B.r[1], pr, split);
           f32x16 gp;
           ucarry = gpath_tile(dz, ucarry, gate, h, gp);
           if constexpr (H0) {   // head 0's dK takes g with its own dz
 #pragma unroll
             for (int i = 0; i < 16; ++i) dz[i] += gp[i];
-            acc_t(dkt, B.t[0], dz, split || big_tile(dz));
+            acc_t(dkt, B.r[0], dz, split || big_tile(dz));
           } else {
-            acc_t(dkt, B.t[0], dz, split);
-            acc_t(dk0t, B.t[2], gp, big_tile(gp));
+            acc_t(dkt, B.r[0], dz, split);
+            acc_t(dk0t, B.r[2], gp, big_tile(gp));
           }
         };
         body();
@@ -2339,8 +2379,8 @@ __global__ __launch_bounds__(NTHREADS, 2) void bwd_kv64_kernel(
     run(0, n_int, std::true_type{});
     run(n_int, ntiles, std::false_type{});
   };
-  if (has_h0) sweep(std::true_type{});
-  else sweep(std::false_type{});
+  if (SOLO || has_h0) sweep(std::true_type{});
+  else if constexpr (!SOLO) sweep(std::false_type{});
 
   if (j >= T) return;
   // dV and the dK of heads other than 0 go to the caller's views; head 0's dK to its fp32 sums,
@@ -3348,13 +3388,12 @@ void launch_kv_from(const KvLaunch& a) {
                      a.scale);
 }
 
-template <bool CV>
+template <bool CV, bool SOLO>
 void launch_kv64_from(const KvLaunch& a) {
   dim3 grid((unsigned)cdiv(a.T, NWAVES * TILE), (unsigned)(a.nseq * a.H));
-  hipLaunchKernelGGL((bwd_kv64_kernel<CV>), grid, dim3(NTHREADS), 0, a.st, static_cast<const uint16_t*>(a.q),
+  hipLaunchKernelGGL((bwd_kv64_kernel<CV, SOLO>), grid, dim3(NTHREADS), 0, a.st, static_cast<const uint16_t*>(a.q),
                      static_cast<const uint16_t*>(a.k), static_cast<const uint16_t*>(a.v),
-                     static_cast<const uint16_t*>(a.qt), static_cast<const uint16_t*>(a.dout),
-                     static_cast<const uint16_t*>(a.dot), a.qs, a.ks, a.vs, a.dos, a.lse, a.dbar, a.carry, a.ucheck,
+                     static_cast<const uint16_t*>(a.dout), a.qs, a.ks, a.vs, a.dos, a.lse, a.dbar, a.carry, a.ucheck,
                      a.dk0h, a.dk0x, a.dkv, a.dvv, a.nseq, a.H, a.T, a.ldt, a.exempt, a.scale);
 }
 
@@ -3442,11 +3481,12 @@ int backward_impl(const BwdCall& c) {
   const elem* k = static_cast<const elem*>(c.k);
   const elem* dout = static_cast<const elem*>(c.dout);
 
-  // bf16 at head dim 64: Q^T and dO^T in the column order of the key side's direct loads
-  // (bwd_kv64_kernel)
-  const bool crow = sizeof(elem) == 2 && D == 64;
-  launch_transpose<elem, D>(q, qt, T, ldt, c.qs, H, R, st, crow);
-  launch_transpose<elem, D>(dout, dot, T, ldt, c.dos, H, R, st, crow);
+  // bf16 at head dim 64 the key side reads its Q, dO rows transposed from LDS (bwd_kv64_kernel):
+  // no Q^T, dO^T copies
+  if constexpr (!(sizeof(elem) == 2 && D == 64)) {
+    launch_transpose<elem, D>(q, qt, T, ldt, c.qs, H, R, st);
+    launch_transpose<elem, D>(dout, dot, T, ldt, c.dos, H, R, st);
+  }
   launch_transpose<elem, D>(k, kt, T, ldt, c.ks, H, R, st);
   hipLaunchKernelGGL((bwd_rowstats_kernel<OP, D>), dim3((unsigned)cdiv(R * ldt * (D / 8), NTHREADS)),
                      dim3(NTHREADS), 0, st, dout, c.dos, H, T, c.out, c.rmax, c.rden, lse, dbar, ldt, R * ldt,

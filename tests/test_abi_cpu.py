@@ -46,11 +46,18 @@ def test_workspace_sizes():
     fw = lib.sa_forward_workspace_bytes(1, 16, 16384, 64, 0)
     assert fw >= 16 * 64 * 16384 * 2 and fw % 256 == 0
     bw = lib.sa_backward_workspace_bytes(1, 16, 16384, 64, 0, 0)
-    # Q^T, dO^T, K^T (bf16), the 16 head groups' U checkpoints (the causal part of each 512 x 16384
-    # plane: 32 x 512 x 513 / 2 floats), head 0's fp32 dq and dk (and the other groups' shares)
+    # K^T (bf16; at head dim 64 the key side reads Q, dO transposed from LDS, so no Q^T, dO^T), the
+    # 16 head groups' U checkpoints (the causal part of each 512 x 16384 plane: 32 x 512 x 513 / 2
+    # floats), head 0's fp32 dq and dk (and the other groups' shares), lse and -dbar
     tri = 16 * 512 * 513
-    assert bw >= 3 * 16 * 64 * 16384 * 2 + 16 * tri * 4 + 4 * 16384 * 64 * 4 and bw % 256 == 0
-    assert bw < 3 * 16 * 64 * 16384 * 2 + 16 * tri * 4 + 4 * 16384 * 64 * 4 + 2 * 16 * 16384 * 4 + 4096
+    fixed = 16 * tri * 4 + 4 * 16384 * 64 * 4 + 2 * 16 * 16384 * 4
+    assert bw >= 16 * 64 * 16384 * 2 + fixed and bw % 256 == 0
+    assert bw < 16 * 64 * 16384 * 2 + fixed + 4096
+    # other head dims (and fp32 storage) keep the Q^T and dO^T copies
+    bw32 = lib.sa_backward_workspace_bytes(1, 16, 16384, 32, 0, 1)
+    assert bw32 >= 3 * 16 * 32 * 16384 * 2 + 16 * tri * 4
+    bwf = lib.sa_backward_workspace_bytes(1, 16, 16384, 64, 1, 0)
+    assert bwf >= 3 * 16 * 64 * 16384 * 4 + fixed
     dw = lib.sa_decode_workspace_bytes(1, 16, 131072, 64)
     assert dw >= 16 * (131072 // 64) * 66 * 4 and dw % 256 == 0   # one (m, l, o[64]) per 64 keys and head
     assert lib.sa_decode_workspace_bytes(0, 16, 100, 64) < 0
