@@ -112,12 +112,12 @@ inline BwdLayout bwd_layout(int64_t nseq, int64_t heads, int64_t t, int64_t D, i
   BwdLayout L;
   int64_t off = 0;
   auto take = [&](int64_t bytes) { int64_t o = off; off = align_up(off + bytes, 256); return o; };
-  // Q^T, dO^T: read by the key side except at bf16 head dim 64, whose kernel reads its Q, dO rows
-  // transposed from LDS
+  // Q^T, dO^T, K^T: none at bf16 head dim 64, whose kernels read the Q, dO and K rows transposed
+  // from LDS
   const int64_t tcopy = (esize == 2 && D == 64) ? 0 : R * D * ldt * esize;
   L.qt = take(tcopy);
   L.dot = take(tcopy);
-  L.kt = take(R * D * ldt * esize);
+  L.kt = take(tcopy);
   L.lse = take(R * ldt * 4);    // (R, ldt): rows padded per head
   L.dbar = take(R * ldt * 4);   // -dbar, likewise
   L.dq = take(nseq * t * D * 4);   // head 0's own fp32 sums (the other heads write their views)

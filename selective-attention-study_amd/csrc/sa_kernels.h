@@ -415,20 +415,22 @@ __device__ __forceinline__ void g2l_rowsq(uint16_t* tile, __amdgpu_buffer_rsrc_t
   __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_void_ptr)(tile + 512 * m), 16, (m & 1) ? rl.v1 : rl.v0,
                                            (row0 + 8 * m) * ld * 2, 0, 0);
 }
-// The A operand of K step s of a product over the rows of a [32 rows][64] swzq tile (Y^T X with Y
-// the tile and X a C-layout tile entering as the B operand, OpBF16::from_acc): lane l gets column
-// 32 db + l % 32 of the tile at the rows X's fragment holds, in the accumulator's row order:
-// element e is row crow(8s + e, l / 32) = 16s + 8(e / 4) + 4(l / 32) + e % 4. Two transposing
-// reads (e / 4 = 0, 1): lane i of a 16-lane group gets, as element t, element i % 4 of the 8 bytes
-// that lane 4t + i/4 of the group addresses, so lane k of the group addresses row base + k/4,
-// columns 4 (k mod 4) .. +3 of the group's 16 (measured lane layout, see get_tr).
+// An operand of K step s of a product over the rows of a [32 rows][64] swzq tile Y (Y^T X, or X Y):
+// lane l gets column 32 db + l % 32 of the tile, rows 16s + 8(l / 32) + 0..7 in order, or with
+// CROW the rows a C-layout tile's fragment holds in the accumulator's row order (X entering from
+// registers, OpBF16::from_acc): element e is row crow(8s + e, l / 32) = 16s + 8(e / 4) + 4(l / 32)
+// + e % 4. Two transposing reads, four rows each: lane i of a 16-lane group gets, as element t,
+// element i % 4 of the 8 bytes that lane 4t + i/4 of the group addresses, so lane k of the group
+// addresses row base + k/4, columns 4 (k mod 4) .. +3 of the group's 16 (measured lane layout, see
+// get_tr).
+template <bool CROW>
 __device__ __forceinline__ bf16x8 get_trq(const uint16_t* t, int lane, int db, int s) {
   const int g = lane >> 4, k = lane & 15;
   const int c = 4 * db + 2 * (g & 1) + ((k & 3) >> 1);   // the 16-byte chunk of the lane's 4 columns
   bf16x8 f;
 #pragma unroll
   for (int hf = 0; hf < 2; ++hf) {
-    const int r = 16 * s + 8 * hf + 4 * (g >> 1) + (k >> 2);
+    const int r = CROW ? 16 * s + 8 * hf + 4 * (g >> 1) + (k >> 2) : 16 * s + 8 * (g >> 1) + 4 * hf + (k >> 2);
     typedef __attribute__((address_space(3))) short4v* lds_s4;
     const short4v v = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s4)(t + swzq(r, c) + 4 * (k & 1)));
 #pragma unroll
@@ -2286,14 +2288,14 @@ __global__ __launch_bounds__(NTHREADS, 2) void bwd_kv64_kernel(
 #pragma unroll
     for (int db = 0; db < DB; ++db)
 #pragma unroll
-      for (int s = 0; s < AS; ++s) acc[db] = OP::mma(get_trq(y, lane, db, s), xf[s], acc[db]);
+      for (int s = 0; s < AS; ++s) acc[db] = OP::mma(get_trq<true>(y, lane, db, s), xf[s], acc[db]);
     if (split) {
 #pragma unroll
       for (int s = 0; s < AS; ++s) xf[s] = OP::from_acc_lo(x, s);
 #pragma unroll
       for (int db = 0; db < DB; ++db)
 #pragma unroll
-        for (int s = 0; s < AS; ++s) acc[db] = OP::mma(get_trq(y, lane, db, s), xf[s], acc[db]);
+        for (int s = 0; s < AS; ++s) acc[db] = OP::mma(get_trq<true>(y, lane, db, s), xf[s], acc[db]);
     }
   };
   // fragment s of row n of a swzq tile (A operand: lane = query row; or B: lane = key)
@@ -2732,28 +2734,30 @@ __global__ __launch_bounds__(NTHREADS, (dq_min_blocks<OP, D>())) void bwd_dq_ker
 
 // ---------------------------------------------------------------------------------------------
 // Backward, query side, bf16 storage at head dim 64 with one head per wavefront: bwd_dq_kernel's
-// tile work with every key tile's operands -- the K, V and head 0's K rows (swz64), K^T and head
-// 0's K^T (swz32), and each wavefront's carry and selection-suffix checkpoint values of the tile's
-// keys -- loaded straight into LDS one tile ahead, two buffers as separate LDS variables (see
-// bwd_kv64_kernel); one barrier per tile. Eight wavefronts (256 queries) per workgroup, one
+// tile work with every key tile's operands -- the K, V and head 0's K rows (swzq; the K rows read
+// as rows by the logit products and transposed by the dQ products, so no K^T is loaded), and each
+// wavefront's carry and selection-suffix checkpoint values of the tile's keys -- loaded straight
+// into LDS one tile ahead, two buffers as separate LDS variables (see bwd_kv64_kernel); one barrier
+// per tile. Eight wavefronts (256 queries) per workgroup, one
 // workgroup per CU: each key tile is staged once for twice the queries of a four-wavefront group
 // (measured 3% faster; the operand staging, not its latency, is what the loads cost).
 
 constexpr int DQ64_WAVES = 8;
 
 struct DqTileBuf64 {
-  __attribute__((aligned(16))) uint16_t k[2][TILE * 64];    // K rows, head 0's K rows
-  __attribute__((aligned(16))) uint16_t v[TILE * 64];       // V rows
-  __attribute__((aligned(16))) uint16_t kt[2][TILE * 64];   // K^T, head 0's K^T
+  __attribute__((aligned(16))) uint16_t k[2][TILE * 64];    // K rows, head 0's K rows (swzq)
+  __attribute__((aligned(16))) uint16_t v[TILE * 64];       // V rows (swzq)
   __attribute__((aligned(16))) float hist[DQ64_WAVES][64];   // per wavefront: each lane's key's carry
   __attribute__((aligned(16))) float uin[DQ64_WAVES][64];    // ... and its U checkpoint
 };
 
-template <bool CV>   // CV: every view is the contiguous (nseq, H, T, D) layout of sa_backward
+// CV: every view is the contiguous (nseq, H, T, D) layout of sa_backward. SOLO: one-head sequences
+// only (head 0's loop alone is built, as in bwd_kv64_kernel).
+template <bool CV, bool SOLO>
 __global__ __launch_bounds__(DQ64_WAVES * 64, 1) void bwd_dq64_kernel(
     const uint16_t* __restrict__ q, const uint16_t* __restrict__ k, const uint16_t* __restrict__ v,
-    const uint16_t* __restrict__ kt, const uint16_t* __restrict__ dout, Strides qs, Strides ks, Strides vs,
-    Strides dos, const float* __restrict__ lse, const float* __restrict__ dbar, const float* __restrict__ carry,
+    const uint16_t* __restrict__ dout, Strides qs, Strides ks, Strides vs, Strides dos,
+    const float* __restrict__ lse, const float* __restrict__ dbar, const float* __restrict__ carry,
     const float* __restrict__ ucheck, float* __restrict__ dq0h, float* __restrict__ dq0x, GradView dqv, int nseq,
     int H, int T, int64_t ldt, int exempt, float scale) {
   using OP = OpBF16;
@@ -2823,38 +2827,33 @@ __global__ __launch_bounds__(DQ64_WAVES * 64, 1) void bwd_dq64_kernel(
   const __amdgpu_buffer_rsrc_t rs_k = rsrc(view_head(k, ks, hh), (int64_t)T * k_ld * 2);
   const __amdgpu_buffer_rsrc_t rs_k0 = rsrc(view_head(k, ks, 0), (int64_t)T * k_ld * 2);
   const __amdgpu_buffer_rsrc_t rs_v = rsrc(view_head(v, vs, hh), (int64_t)T * v_ld * 2);
-  const __amdgpu_buffer_rsrc_t rs_kt = rsrc(kt + (seq_row + hh) * D * ldt, (int64_t)D * ldt * 2);
-  const __amdgpu_buffer_rsrc_t rs_k0t = rsrc(kt + seq_row * D * ldt, (int64_t)D * ldt * 2);
   const __amdgpu_buffer_rsrc_t rs_c = rsrc(carry + ((int64_t)b * NB + qb_c) * T, (int64_t)T * 4);
   const __amdgpu_buffer_rsrc_t rs_u =
       rsrc(ucheck + ((int64_t)hh * nseq + b) * utri_floats(NB) + utri_row(qb_c), (int64_t)(qb_c + 1) * TILE * 4);
-  const RowsLane rl_k(k_ld, lane), rl_v(v_ld, lane);
-  const int cl = cols_lane(ldt, lane);
+  const RowsLaneQ rl_k(k_ld, lane), rl_v(v_ld, lane);
 
   // everything key tile ktile needs, into buffer B, by direct loads only (see bwd_kv64_kernel):
-  // wavefronts 0-3 load a quarter of each row tile, 4-7 of each transposed one
+  // wavefronts 0-3 load a quarter of the K rows (and of head 0's), 4-7 of the V rows
   auto load_tile = [&](int ktile, DqTileBuf64& B) {
     const int kbase = ktile * TILE;
     const int m = wave & 3;
     if (wave < 4) {
-      g2l_rows64(B.k[0], rs_k, rl_k, k_ld, kbase, m);
-      g2l_rows64(B.v, rs_v, rl_v, v_ld, kbase, m);
-      if (!has_h0) g2l_rows64(B.k[1], rs_k0, rl_k, k_ld, kbase, m);
+      g2l_rowsq(B.k[0], rs_k, rl_k, k_ld, kbase, m);
+      if (!has_h0) g2l_rowsq(B.k[1], rs_k0, rl_k, k_ld, kbase, m);
     } else {
-      g2l_cols32(B.kt[0], rs_kt, cl, (int)ldt, kbase, m);
-      if (!has_h0) g2l_cols32(B.kt[1], rs_k0t, cl, (int)ldt, kbase, m);
+      g2l_rowsq(B.v, rs_v, rl_v, v_ld, kbase, m);
     }
     const int jo = (kbase + n) * 4;
     __builtin_amdgcn_raw_ptr_buffer_load_lds(rs_c, (lds_void_ptr)B.hist[wave], 4, jo, 0, 0, 0);
     __builtin_amdgcn_raw_ptr_buffer_load_lds(rs_u, (lds_void_ptr)B.uin[wave], 4, jo, 0, 0, 0);
   };
-  // fragment s of row n (lane = key) of a swz64 tile
+  // fragment s of row n (lane = key) of a swzq tile
   auto rfrag = [&](const elem* tile, int s) -> frag {
-    return *reinterpret_cast<const frag*>(tile + swz64(n, 2 * s + h));
+    return *reinterpret_cast<const frag*>(tile + swzq(n, 2 * s + h));
   };
   // acc[db] (queries x D) += X K: X a C-layout (queries x keys) tile sent through the wavefront's
-  // LDS tile to become the A operand (transposed write, transposing read), K^T (swz32) the B
-  // operand; with split, X's rounding residual takes a second pass.
+  // LDS tile to become the A operand (transposed write, transposing read), the K rows (swzq) read
+  // transposed as the B operand; with split, X's rounding residual takes a second pass.
   auto acc_xk = [&](f32x16 (&acc)[DB], const f32x16& x, const elem* ktile, bool split) {
     frag zf[AS];
     put_tr<false>(zs, x, n, h);
@@ -2865,7 +2864,7 @@ __global__ __launch_bounds__(DQ64_WAVES * 64, 1) void bwd_dq64_kernel(
     for (int db = 0; db < DB; ++db)
 #pragma unroll
       for (int s = 0; s < AS; ++s)
-        acc[db] = OP::mma(zf[s], *reinterpret_cast<const frag*>(ktile + swz32(db * 32 + n, 2 * s + h)), acc[db]);
+        acc[db] = OP::mma(zf[s], get_trq<false>(ktile, lane, db, s), acc[db]);
     if (split) {
       lds_wave_sync();
       put_tr<true>(zs, x, n, h);
@@ -2876,7 +2875,7 @@ __global__ __launch_bounds__(DQ64_WAVES * 64, 1) void bwd_dq64_kernel(
       for (int db = 0; db < DB; ++db)
 #pragma unroll
         for (int s = 0; s < AS; ++s)
-          acc[db] = OP::mma(zf[s], *reinterpret_cast<const frag*>(ktile + swz32(db * 32 + n, 2 * s + h)), acc[db]);
+          acc[db] = OP::mma(zf[s], get_trq<false>(ktile, lane, db, s), acc[db]);
     }
     lds_wave_sync();
   };
@@ -2928,10 +2927,10 @@ __global__ __launch_bounds__(DQ64_WAVES * 64, 1) void bwd_dq64_kernel(
         if constexpr (H0) {   // head 0's dQ takes g with its own dz
 #pragma unroll
           for (int i = 0; i < 16; ++i) dz[i] += gp[i];
-          acc_xk(dqacc, dz, B.kt[0], big_tile(dz));
+          acc_xk(dqacc, dz, B.k[0], big_tile(dz));
         } else {
-          acc_xk(dqacc, dz, B.kt[0], false);
-          acc_xk(dq0acc, gp, B.kt[1], big_tile(gp));
+          acc_xk(dqacc, dz, B.k[0], false);
+          acc_xk(dq0acc, gp, B.k[1], big_tile(gp));
         }
       }
       wait_loads();
@@ -2954,8 +2953,8 @@ __global__ __launch_bounds__(DQ64_WAVES * 64, 1) void bwd_dq64_kernel(
     run(i_lo, i_hi, std::true_type{});
     run(i_hi, wg_end, std::false_type{});
   };
-  if (has_h0) sweep(std::true_type{});
-  else sweep(std::false_type{});
+  if (SOLO || has_h0) sweep(std::true_type{});
+  else if constexpr (!SOLO) sweep(std::false_type{});
 
   if (qb >= NB) return;
   // heads other than 0: dQ (scaled) to the caller's view; head 0: unscaled fp32 sums, where the
@@ -3441,12 +3440,17 @@ int launch_bwd(const BwdCall& c, const typename OP::elem* qt, const typename OP:
     TimedLaunch timed(SA_KERNEL_BACKWARD_DQ, c.st);
     if constexpr (sizeof(elem) == 2 && D == 64 && G == 1) {   // one head per wavefront: the pipelined kernel
       const dim3 grid64((unsigned)cdiv(c.T, DQ64_WAVES * TILE), (unsigned)(c.nseq * c.H));
-#define SA_LAUNCH_DQ64(CVV)                                                                                        \
-  hipLaunchKernelGGL((bwd_dq64_kernel<CVV>), grid64, dim3(DQ64_WAVES * 64), 0, c.st, q, k, v, kt, dout, c.qs,    \
-                     c.ks, c.vs,                                                                                   \
-                     c.dos, lse, dbar, c.carry, ucheck, dq0h, dq0x, dqv, c.nseq, c.H, c.T, ldt, c.exempt, c.scale)
-      if (cv) SA_LAUNCH_DQ64(true);
-      else SA_LAUNCH_DQ64(false);
+#define SA_LAUNCH_DQ64(CVV, SOLO)                                                                                  \
+  hipLaunchKernelGGL((bwd_dq64_kernel<CVV, SOLO>), grid64, dim3(DQ64_WAVES * 64), 0, c.st, q, k, v, dout, c.qs, c.ks, \
+                     c.vs, c.dos, lse, dbar, c.carry, ucheck, dq0h, dq0x, dqv, c.nseq, c.H, c.T, ldt, c.exempt,    \
+                     c.scale)
+      if (c.H == 1) {   // one-head sequences: head 0's loop only
+        if (cv) SA_LAUNCH_DQ64(true, true);
+        else SA_LAUNCH_DQ64(false, true);
+      } else {
+        if (cv) SA_LAUNCH_DQ64(true, false);
+        else SA_LAUNCH_DQ64(false, false);
+      }
 #undef SA_LAUNCH_DQ64
     } else {
       if (cv) SA_LAUNCH_DQ(true);
@@ -3481,13 +3485,13 @@ int backward_impl(const BwdCall& c) {
   const elem* k = static_cast<const elem*>(c.k);
   const elem* dout = static_cast<const elem*>(c.dout);
 
-  // bf16 at head dim 64 the key side reads its Q, dO rows transposed from LDS (bwd_kv64_kernel):
-  // no Q^T, dO^T copies
+  // bf16 at head dim 64 the backward kernels read their Q, dO and K rows transposed from LDS
+  // (bwd_kv64_kernel, bwd_dq64_kernel): no transposed copies
   if constexpr (!(sizeof(elem) == 2 && D == 64)) {
     launch_transpose<elem, D>(q, qt, T, ldt, c.qs, H, R, st);
     launch_transpose<elem, D>(dout, dot, T, ldt, c.dos, H, R, st);
+    launch_transpose<elem, D>(k, kt, T, ldt, c.ks, H, R, st);
   }
-  launch_transpose<elem, D>(k, kt, T, ldt, c.ks, H, R, st);
   hipLaunchKernelGGL((bwd_rowstats_kernel<OP, D>), dim3((unsigned)cdiv(R * ldt * (D / 8), NTHREADS)),
                      dim3(NTHREADS), 0, st, dout, c.dos, H, T, c.out, c.rmax, c.rden, lse, dbar, ldt, R * ldt,
                      // head 0's shares from the other groups are atomic targets (one add per element

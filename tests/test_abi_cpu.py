@@ -46,14 +46,14 @@ def test_workspace_sizes():
     fw = lib.sa_forward_workspace_bytes(1, 16, 16384, 64, 0)
     assert fw >= 16 * 64 * 16384 * 2 and fw % 256 == 0
     bw = lib.sa_backward_workspace_bytes(1, 16, 16384, 64, 0, 0)
-    # K^T (bf16; at head dim 64 the key side reads Q, dO transposed from LDS, so no Q^T, dO^T), the
-    # 16 head groups' U checkpoints (the causal part of each 512 x 16384 plane: 32 x 512 x 513 / 2
-    # floats), head 0's fp32 dq and dk (and the other groups' shares), lse and -dbar
+    # the 16 head groups' U checkpoints (the causal part of each 512 x 16384 plane: 32 x 512 x 513 / 2
+    # floats), head 0's fp32 dq and dk (and the other groups' shares), lse and -dbar; no transposed
+    # copies (at bf16 head dim 64 the kernels read Q, dO and K transposed from LDS)
     tri = 16 * 512 * 513
     fixed = 16 * tri * 4 + 4 * 16384 * 64 * 4 + 2 * 16 * 16384 * 4
-    assert bw >= 16 * 64 * 16384 * 2 + fixed and bw % 256 == 0
-    assert bw < 16 * 64 * 16384 * 2 + fixed + 4096
-    # other head dims (and fp32 storage) keep the Q^T and dO^T copies
+    assert bw >= fixed and bw % 256 == 0
+    assert bw < fixed + 4096
+    # other head dims (and fp32 storage) keep the Q^T, dO^T and K^T copies
     bw32 = lib.sa_backward_workspace_bytes(1, 16, 16384, 32, 0, 1)
     assert bw32 >= 3 * 16 * 32 * 16384 * 2 + 16 * tri * 4
     bwf = lib.sa_backward_workspace_bytes(1, 16, 16384, 64, 1, 0)
