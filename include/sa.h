@@ -75,8 +75,10 @@ int sa_timing_read(int kernel, double* total_ms, int64_t* launches);
 /* Leading dimension (elements) of the transposed copies held in the workspaces. */
 int64_t sa_transposed_ld(int64_t t);
 
-/* Bytes of scratch sa_forward needs (the transposed value copy). */
-int64_t sa_forward_workspace_bytes(int64_t nseq, int64_t heads, int64_t tk, int64_t head_dim, int dtype);
+/* Bytes of scratch sa_forward needs for the same `group` argument: the transposed value copy, or 0
+ * for bf16 at head dim 64 with one or two heads per wavefront (the default there), whose kernel
+ * reads the value rows themselves (workspace may then be NULL). */
+int64_t sa_forward_workspace_bytes(int64_t nseq, int64_t heads, int64_t tk, int64_t head_dim, int dtype, int group);
 
 /*
  * Forward pass, and one chunk of a chunked prefill.

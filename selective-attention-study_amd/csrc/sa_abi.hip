@@ -68,8 +68,11 @@ const char* sa_status_string(int status) {
 
 int64_t sa_transposed_ld(int64_t t) { return align_up(t < 1 ? 1 : t, 64); }
 
-int64_t sa_forward_workspace_bytes(int64_t nseq, int64_t heads, int64_t tk, int64_t head_dim, int dtype) {
+// The forward's scratch is the transposed value copy fwd_kernel reads; none where fwd64_kernel runs
+// (bf16 at head dim 64, one or two heads per wavefront: it reads the V rows themselves).
+int64_t sa_forward_workspace_bytes(int64_t nseq, int64_t heads, int64_t tk, int64_t head_dim, int dtype, int group) {
   const int64_t es = dtype == SA_DTYPE_BF16 ? 2 : 4;
+  if (dtype == SA_DTYPE_BF16 && head_dim == 64 && auto_group(dtype, head_dim, heads, group, false) <= 2) return 0;
   return align_up(nseq * heads * head_dim * sa_transposed_ld(tk) * es, 256);
 }
 
@@ -110,7 +113,7 @@ int sa_forward_strided(const void* q, const sa_view_strides* q_strides, const vo
                        int64_t q_offset, int64_t head_dim, float scale, int dtype, int exempt, int group,
                        int damp_mode, int64_t train_len, void* stream) {
   if (!valid_dims(nseq, heads, tk) || tq < 1 || q_offset < 0 || q_offset + tq != tk) return SA_ERR_ARGUMENT;
-  if (!q || !k || !v || !out || !rmax || !rden || !carry || !state_out || !workspace) return SA_ERR_ARGUMENT;
+  if (!q || !k || !v || !out || !rmax || !rden || !carry || !state_out) return SA_ERR_ARGUMENT;
   if (q_offset > 0 && !state_in) return SA_ERR_ARGUMENT;
   if (state_ld < tk || exempt < 1 || damp_mode < 0 || damp_mode > 2 || (damp_mode && train_len < 1))
     return SA_ERR_ARGUMENT;
@@ -121,7 +124,8 @@ int sa_forward_strided(const void* q, const sa_view_strides* q_strides, const vo
       !view_ok(v_strides, tk, head_dim, dtype, false) || (y && !view_ok(y_strides, tq, head_dim, dtype, true)))
     return SA_ERR_ARGUMENT;
   if (((uintptr_t)q | (uintptr_t)k | (uintptr_t)v | (uintptr_t)y) % 16) return SA_ERR_ARGUMENT;
-  if (workspace_bytes < sa_forward_workspace_bytes(nseq, heads, tk, head_dim, dtype)) return SA_ERR_WORKSPACE;
+  const int64_t need = sa_forward_workspace_bytes(nseq, heads, tk, head_dim, dtype, group);
+  if (workspace_bytes < need || (need > 0 && !workspace)) return SA_ERR_WORKSPACE;
   auto st = [](const sa_view_strides* p) { return p ? Strides{p->seq, p->head, (int)p->row} : Strides{0, 0, 0}; };
   FwdCall c{};
   c.q = q;

@@ -1190,16 +1190,16 @@ __global__ __launch_bounds__(NTHREADS, (fwd_min_blocks<OP, D, G>())) void fwd_ke
 // start of tile t + 1), so each tile is one block of independent products and arithmetic the
 // compiler interleaves, with no wait inside it for the F round trip. A one-head group holding head 0
 // sends that head's whole adjusted logits through the LDS rows instead (as fwd_kernel does), so it
-// takes one logit product per tile. The K rows of the group's heads and their V^T (swz64 / swz32)
-// load one tile ahead into two buffers; head 0's K rows and each wavefront's carry row two tiles
+// takes one logit product per tile. The K rows of the group's heads (swz64) and their V rows (swzq,
+// read transposed by the value products, get_trq) load one tile ahead into two buffers; head 0's K rows and each wavefront's carry row two tiles
 // ahead into two more; all four are separate LDS variables and the tile loop runs in pairs, so every
 // access names its buffer at compile time; one barrier per tile. Two workgroups per CU at G = 2,
 // three at G = 1.
 
 template <int G>
 struct FwdTileBuf64 {
-  __attribute__((aligned(16))) uint16_t k[G][TILE * 64];    // K rows of the group's heads
-  __attribute__((aligned(16))) uint16_t vt[G][TILE * 64];   // their V^T
+  __attribute__((aligned(16))) uint16_t k[G][TILE * 64];   // K rows of the group's heads
+  __attribute__((aligned(16))) uint16_t v[G][TILE * 64];   // their V rows
 };
 struct FwdSelBuf64 {
   __attribute__((aligned(16))) uint16_t k0[TILE * 64];      // head 0's K rows
@@ -1208,16 +1208,16 @@ struct FwdSelBuf64 {
 
 template <bool CV, int G>   // CV: as fwd_kernel; G: heads per wavefront (1 or 2)
 __global__ __launch_bounds__(NTHREADS, G == 1 ? 3 : 2) void fwd64_kernel(
-    const uint16_t* __restrict__ q, const uint16_t* __restrict__ k, const uint16_t* __restrict__ vt,
+    const uint16_t* __restrict__ q, const uint16_t* __restrict__ k, const uint16_t* __restrict__ v,
     const float* __restrict__ carry, float* __restrict__ out, float* __restrict__ rmax, float* __restrict__ rden,
-    uint16_t* __restrict__ y, Strides ys, int H, int Tq, int Tk, Strides qs, Strides ks, int q_off, int64_t ldv,
+    uint16_t* __restrict__ y, Strides ys, int H, int Tq, int Tk, Strides qs, Strides ks, Strides vs, int q_off,
     int exempt, float scale, int damp_mode, float train_len) {
   using OP = OpBF16;
   using elem = uint16_t;
   using frag = OP::frag;
   constexpr int D = 64, NS = 4, DB = 2, AS = 2;
   static_assert(G == 1 || G == 2, "one or two heads per wavefront");
-  __shared__ FwdTileBuf64<G> sB0, sB1;   // tile t's K rows and V^T in buffer t mod 2
+  __shared__ FwdTileBuf64<G> sB0, sB1;   // tile t's K and V rows in buffer t mod 2
   __shared__ FwdSelBuf64 sS0, sS1;    // tile t's head-0 K rows and carry rows in buffer t mod 2
   constexpr int LDF = TILE + 4;
   __shared__ __attribute__((aligned(16))) float sF[NWAVES][TILE * LDF];   // each wavefront's F tile
@@ -1294,23 +1294,23 @@ __global__ __launch_bounds__(NTHREADS, G == 1 ? 3 : 2) void fwd64_kernel(
   const __amdgpu_buffer_rsrc_t rs_k0 = rsrc(k_head(hd0), (int64_t)Tk * k_ld * 2);
   const __amdgpu_buffer_rsrc_t rs_k1 = rsrc(k_head(hd0 + G - 1), (int64_t)Tk * k_ld * 2);
   const __amdgpu_buffer_rsrc_t rs_kh = rsrc(k_head(0), (int64_t)Tk * k_ld * 2);
-  const __amdgpu_buffer_rsrc_t rs_v0 = rsrc(vt + (seq_row + hd0) * D * ldv, (int64_t)D * ldv * 2);
-  const __amdgpu_buffer_rsrc_t rs_v1 = rsrc(vt + (seq_row + hd0 + G - 1) * D * ldv, (int64_t)D * ldv * 2);
+  const __amdgpu_buffer_rsrc_t rs_v0 = rsrc(v + vs.at(b, hd0), (int64_t)Tk * vs.row * 2);
+  const __amdgpu_buffer_rsrc_t rs_v1 = rsrc(v + vs.at(b, hd0 + G - 1), (int64_t)Tk * vs.row * 2);
   // this wavefront's carry row (its query block's; keys past the end read zero)
   const __amdgpu_buffer_rsrc_t rs_c =
       rsrc(carry + ((int64_t)b * NBq + min(rb, NBq - 1)) * Tk, (int64_t)Tk * 4);
   const RowsLane rl_k(k_ld, lane);
-  const int cl = cols_lane(ldv, lane);
+  const RowsLaneQ rl_v(vs.row, lane);
 
-  // key tile kt's K rows and V^T (into B), and its head-0 K rows and carry rows (into S), by direct
+  // key tile kt's K and V rows (into B), and its head-0 K rows and carry rows (into S), by direct
   // loads only
   auto load_tile = [&](int kt, FwdTileBuf64<G>& B) {
     const int kbase = kt * TILE;
     g2l_rows64(B.k[0], rs_k0, rl_k, k_ld, kbase, wave);
-    g2l_cols32(B.vt[0], rs_v0, cl, (int)ldv, kbase, wave);
+    g2l_rowsq(B.v[0], rs_v0, rl_v, vs.row, kbase, wave);
     if constexpr (G == 2) {
       g2l_rows64(B.k[1], rs_k1, rl_k, k_ld, kbase, wave);
-      g2l_cols32(B.vt[1], rs_v1, cl, (int)ldv, kbase, wave);
+      g2l_rowsq(B.v[1], rs_v1, rl_v, vs.row, kbase, wave);
     }
   };
   auto load_sel = [&](int kt, FwdSelBuf64& S) {
@@ -1444,8 +1444,7 @@ __global__ __launch_bounds__(NTHREADS, G == 1 ? 3 : 2) void fwd64_kernel(
         for (int db = 0; db < DB; ++db)
 #pragma unroll
           for (int s = 0; s < AS; ++s)
-            o[g][db] = OP::mma(*reinterpret_cast<const frag*>(B.vt[g] + swz32(db * 32 + n, 2 * s + h)), pf[s],
-                               o[g][db]);
+            o[g][db] = OP::mma(get_trq<true>(B.v[g], lane, db, s), pf[s], o[g][db]);
       }
     }
     // the next tile's F (after this tile's reads of the wavefront's F rows, in program order)
@@ -1591,10 +1590,7 @@ __global__ __launch_bounds__(NTHREADS) void transpose_kernel(const E* __restrict
 // eight 16-byte row loads (t past T read as zero), the block transposed in registers (each output
 // word joins the same half-word of two rows), eight 16-byte column stores. A wavefront's loads and
 // stores cover whole 128-byte segments (eight lanes per row or column).
-// CROW: each output row holds its 16-column blocks in C-layout row order (groups of four columns
-// 0, 2, 1, 3), the order in which a transposed operand tile enters the products of the forward
-// kernel at head dim 64 (V^T), so that its direct loads into LDS are plain copies.
-template <int D, bool CROW>
+template <int D>
 __global__ __launch_bounds__(NTHREADS) void transpose8_kernel(const uint16_t* __restrict__ in,
                                                               uint16_t* __restrict__ outT, int T, int64_t ldt,
                                                               Strides is, int H) {
@@ -1620,33 +1616,19 @@ __global__ __launch_bounds__(NTHREADS) void transpose8_kernel(const uint16_t* __
       const uint32_t lo = word(2 * w, e >> 1), hi = word(2 * w + 1, e >> 1);
       o[w] = (e & 1) ? ((lo >> 16) | (hi & 0xFFFF0000u)) : ((lo & 0xFFFFu) | (hi << 16));
     }
-    uint16_t* row = dst + (int64_t)(8 * c + e) * ldt;
-    if constexpr (CROW) {
-      // t0 % 16 is 0 or 8: its groups of four a = (t0 % 16) / 4 and a + 1 go to 2 (a mod 2) + a / 2
-      const int a = (int)(t0 & 15) >> 2;
-      uint16_t* blk = row - (t0 & 15);
-      *reinterpret_cast<uint2*>(blk + 4 * (((a & 1) << 1) | (a >> 1))) = make_uint2(o[0], o[1]);
-      *reinterpret_cast<uint2*>(blk + 4 * ((((a + 1) & 1) << 1) | ((a + 1) >> 1))) = make_uint2(o[2], o[3]);
-    } else {
-      *reinterpret_cast<uint4*>(row) = make_uint4(o[0], o[1], o[2], o[3]);
-    }
+    *reinterpret_cast<uint4*>(dst + (int64_t)(8 * c + e) * ldt) = make_uint4(o[0], o[1], o[2], o[3]);
   }
 }
 
-// in (R views, Strides is) -> outT (R, D, ldt), ldt a multiple of 64, zero past T; crow (2-byte
-// elements): columns in C-layout row order within each 16-column block (transpose8_kernel).
+// in (R views, Strides is) -> outT (R, D, ldt), ldt a multiple of 64, zero past T.
 template <typename E, int D>
 void launch_transpose(const E* in, E* outT, int T, int64_t ldt, const Strides& is, int H, int64_t R,
-                      hipStream_t st, bool crow = false) {
+                      hipStream_t st) {
   if constexpr (sizeof(E) == 2) {
     constexpr int rows_per_block = NTHREADS / (D / 8) * 8;
     const dim3 grid((unsigned)cdiv(ldt, rows_per_block), (unsigned)R);
-    if (crow)
-      hipLaunchKernelGGL((transpose8_kernel<D, true>), grid, dim3(NTHREADS), 0, st,
-                         reinterpret_cast<const uint16_t*>(in), reinterpret_cast<uint16_t*>(outT), T, ldt, is, H);
-    else
-      hipLaunchKernelGGL((transpose8_kernel<D, false>), grid, dim3(NTHREADS), 0, st,
-                         reinterpret_cast<const uint16_t*>(in), reinterpret_cast<uint16_t*>(outT), T, ldt, is, H);
+    hipLaunchKernelGGL((transpose8_kernel<D>), grid, dim3(NTHREADS), 0, st, reinterpret_cast<const uint16_t*>(in),
+                       reinterpret_cast<uint16_t*>(outT), T, ldt, is, H);
   } else {
     hipLaunchKernelGGL((transpose_kernel<E, D>), dim3((unsigned)cdiv(ldt, 64), (unsigned)R), dim3(NTHREADS), 0, st,
                        in, outT, T, ldt, is, H);
@@ -3325,7 +3307,7 @@ int run_selection(const FwdCall& c, hipStream_t st) {
 }
 
 template <class OP, int D, int G>
-void launch_fwd(const FwdCall& c, const typename OP::elem* vt, int64_t ldv) {
+void launch_fwd(const FwdCall& c, const typename OP::elem* vt, int64_t ldv) {   // vt: V^T (fwd_kernel only)
   using elem = typename OP::elem;
   const int NBq = (int)cdiv(c.Tq, TILE);
   dim3 grid((unsigned)cdiv(NBq, NWAVES), (unsigned)(c.nseq * (c.H / G)));
@@ -3336,8 +3318,9 @@ void launch_fwd(const FwdCall& c, const typename OP::elem* vt, int64_t ldv) {
   if constexpr (sizeof(elem) == 2 && D == 64 && G <= 2) {   // the direct-load kernel
 #define SA_LAUNCH_FWD64(CVV)                                                                                      \
   hipLaunchKernelGGL((fwd64_kernel<CVV, G>), grid, dim3(NTHREADS), 0, c.st, static_cast<const elem*>(c.q),       \
-                     static_cast<const elem*>(c.k), vt, c.carry, c.out, c.rmax, c.rden, static_cast<elem*>(c.y),  \
-                     c.ys, c.H, c.Tq, c.Tk, c.qs, c.ks, c.q_off, ldv, c.exempt, c.scale, c.damp_mode, c.train_len)
+                     static_cast<const elem*>(c.k), static_cast<const elem*>(c.v), c.carry, c.out, c.rmax,        \
+                     c.rden, static_cast<elem*>(c.y), c.ys, c.H, c.Tq, c.Tk, c.qs, c.ks, c.vs, c.q_off, c.exempt, \
+                     c.scale, c.damp_mode, c.train_len)
     if (cv) SA_LAUNCH_FWD64(true);
     else SA_LAUNCH_FWD64(false);
 #undef SA_LAUNCH_FWD64
@@ -3359,10 +3342,10 @@ int forward_impl(const FwdCall& c) {
   elem* vt = static_cast<elem*>(c.ws);
   const int dtype = sizeof(elem) == 2 ? SA_DTYPE_BF16 : SA_DTYPE_F32;
   const int G = auto_group(dtype, D, c.H, c.group, false);
-  // V^T in the column order of fwd64_kernel's direct loads when it runs
-  const bool crow = sizeof(elem) == 2 && D == 64 && G <= 2;
-  launch_transpose<elem, D>(static_cast<const elem*>(c.v), vt, c.Tk, ldv, c.vs, c.H, (int64_t)c.nseq * c.H, c.st,
-                            crow);
+  // V^T for fwd_kernel (fwd64_kernel, bf16 at head dim 64 with G <= 2, reads the V rows transposed
+  // from LDS)
+  if (!(sizeof(elem) == 2 && D == 64 && G <= 2))
+    launch_transpose<elem, D>(static_cast<const elem*>(c.v), vt, c.Tk, ldv, c.vs, c.H, (int64_t)c.nseq * c.H, c.st);
   int rc = run_selection<OP, D>(c, c.st);
   if (rc) return rc;
   if (G == 4) {

@@ -44,7 +44,7 @@ SIGNATURES = {
     "sa_transposed_ld": (_I64, [_I64]),
     "sa_timing_enable": (_I, [_I]),
     "sa_timing_read": (_I, [_I, ctypes.POINTER(ctypes.c_double), ctypes.POINTER(_I64)]),
-    "sa_forward_workspace_bytes": (_I64, [_I64, _I64, _I64, _I64, _I]),
+    "sa_forward_workspace_bytes": (_I64, [_I64, _I64, _I64, _I64, _I, _I]),
     "sa_forward": (_I, [_P, _P, _P, _P, _P, _P, _P, _P, _P, _I64, _P, _I64,
                         _I64, _I64, _I64, _I64, _I64, _I64, _I64, _F, _I, _I, _I, _I, _I64, _P]),
     "sa_forward_strided": (_I, [_P, _VS, _P, _VS, _P, _VS, _P, _P, _VS, _P, _P, _P, _P, _P, _I64, _P, _I64,

@@ -220,7 +220,7 @@ def _launch_forward(qs: Tensor, ks: Tensor, vs: Tensor, kstride: int, scale: flo
     carry = torch.empty(batch, nb, tk, device=dev, dtype=torch.float32)
     if state is None:
         state = torch.empty(batch, tk, device=dev, dtype=torch.float32)
-    ws = torch.empty(max(int(lib.sa_forward_workspace_bytes(batch, heads, tk, kdim, code)), 1), device=dev,
+    ws = torch.empty(max(int(lib.sa_forward_workspace_bytes(batch, heads, tk, kdim, code, group)), 1), device=dev,
                      dtype=torch.uint8)
     with torch.cuda.device(dev):
         _lib.check(lib.sa_forward(
@@ -304,7 +304,7 @@ def _qkv_forward_op(qkv: Tensor, heads: int, exempt: int) -> tuple[Tensor, Tenso
     rden = torch.empty(batch, heads, seq, device=dev, dtype=torch.float32)
     carry = torch.empty(batch, (seq + CARRY_M - 1) // CARRY_M, seq, device=dev, dtype=torch.float32)
     state = torch.empty(batch, seq, device=dev, dtype=torch.float32)
-    ws = torch.empty(max(int(lib.sa_forward_workspace_bytes(batch, heads, seq, head_dim, code)), 1), device=dev,
+    ws = torch.empty(max(int(lib.sa_forward_workspace_bytes(batch, heads, seq, head_dim, code, 0)), 1), device=dev,
                      dtype=torch.uint8)
     qkv_s, y_s = _packed_strides(batch, seq, heads, head_dim)
     base = qkv.data_ptr()

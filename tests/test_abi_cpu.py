@@ -43,8 +43,14 @@ def test_status_strings():
 def test_workspace_sizes():
     lib = _lib.load()
     assert lib.sa_transposed_ld(1) == 64 and lib.sa_transposed_ld(64) == 64 and lib.sa_transposed_ld(65) == 128
-    fw = lib.sa_forward_workspace_bytes(1, 16, 16384, 64, 0)
+    # the forward's scratch is V^T, except where the head-dim-64 bf16 kernel (one or two heads per
+    # wavefront, the default) reads the V rows themselves
+    assert lib.sa_forward_workspace_bytes(1, 16, 16384, 64, 0, 0) == 0
+    assert lib.sa_forward_workspace_bytes(1, 15, 16384, 64, 0, 0) == 0
+    fw = lib.sa_forward_workspace_bytes(1, 16, 16384, 64, 0, 4)
     assert fw >= 16 * 64 * 16384 * 2 and fw % 256 == 0
+    assert lib.sa_forward_workspace_bytes(1, 16, 16384, 32, 0, 0) >= 16 * 32 * 16384 * 2
+    assert lib.sa_forward_workspace_bytes(1, 16, 16384, 64, 1, 0) >= 16 * 64 * 16384 * 4
     bw = lib.sa_backward_workspace_bytes(1, 16, 16384, 64, 0, 0)
     # the 16 head groups' U checkpoints (the causal part of each 512 x 16384 plane: 32 x 512 x 513 / 2
     # floats), head 0's fp32 dq and dk (and the other groups' shares), lse and -dbar; no transposed
@@ -127,7 +133,8 @@ def test_invalid_arguments_are_rejected_before_any_launch():
     bad[20] = 7          # dtype
     assert lib.sa_forward(*bad) == -3
     bad = list(args)
-    bad[11] = 16         # workspace too small
+    bad[11] = 16         # workspace too small (four heads per wavefront: fwd_kernel reads V^T)
+    bad[22] = 4
     assert lib.sa_forward(*bad) == -4
     bad = list(args)
     bad[21] = 0          # exempt
