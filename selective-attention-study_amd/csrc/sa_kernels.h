@@ -383,37 +383,38 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t rsrc(const void* p, int64_t by
 //   cols32: a [64 rows][32] tile in swz32 layout, columns col0.. of one of this library's transposed
 //           copies (row stride ld, zero-filled past T). Slot 64m + l holds row 16m + l/4, logical
 //           chunk (l mod 4) ^ (l/16 mod 4).
+// A wavefront always loads the same part m of every tile, so the lane's offset is chosen once, as a
+// value (a per-load choice between two fields compiled into a choice of addresses, which kept the
+// pair in scratch memory and made every load wait for a scratch read first).
 struct RowsLane {
-  int v0, v1;   // the lane's byte offsets for the even and the odd parts
-  __device__ __forceinline__ RowsLane(int ld, int lane) {
+  int v;   // the lane's byte offset for part m
+  __device__ __forceinline__ RowsLane(int ld, int lane, int m) {
     const int c0 = ((lane & 7) - (lane >> 4)) & 7;
-    v0 = ((lane >> 3) * ld + 8 * c0) * 2;
-    v1 = ((lane >> 3) * ld + 8 * (c0 ^ 4)) * 2;
+    v = ((lane >> 3) * ld + 8 * ((m & 1) ? (c0 ^ 4) : c0)) * 2;
   }
 };
 __device__ __forceinline__ int cols_lane(int64_t ld, int lane) {
   return (int)((lane >> 2) * ld + 8 * ((lane & 3) ^ ((lane >> 4) & 3))) * 2;
 }
 __device__ __forceinline__ void g2l_rows64(uint16_t* tile, __amdgpu_buffer_rsrc_t rs, const RowsLane& rl, int ld,
-                                           int row0, int m) {
-  __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_void_ptr)(tile + 512 * m), 16, (m & 1) ? rl.v1 : rl.v0,
-                                           (row0 + 8 * m) * ld * 2, 0, 0);
+                                           int row0, int m) {   // m: the part rl was made for
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_void_ptr)(tile + 512 * m), 16, rl.v, (row0 + 8 * m) * ld * 2, 0,
+                                           0);
 }
 //   rowsq: a [32 rows][64] tile in swzq layout, as rows64. Slot 64m + l holds row r = 8m + l/8,
 //          stored chunk l mod 8, so logical chunk (l mod 8) ^ f(r), f(r) = 2 (l/8 mod 4) ^ (l/32)
 //          ^ 2 (m mod 2): c0 = (l mod 8) ^ 2 (l/8 mod 4) ^ l/32 for even m, c0 ^ 2 for odd m.
 struct RowsLaneQ {
-  int v0, v1;   // the lane's byte offsets for the even and the odd parts
-  __device__ __forceinline__ RowsLaneQ(int ld, int lane) {
+  int v;   // the lane's byte offset for part m (see RowsLane)
+  __device__ __forceinline__ RowsLaneQ(int ld, int lane, int m) {
     const int c0 = (lane & 7) ^ (((lane >> 3) & 3) << 1) ^ (lane >> 5);
-    v0 = ((lane >> 3) * ld + 8 * c0) * 2;
-    v1 = ((lane >> 3) * ld + 8 * (c0 ^ 2)) * 2;
+    v = ((lane >> 3) * ld + 8 * ((m & 1) ? (c0 ^ 2) : c0)) * 2;
   }
 };
 __device__ __forceinline__ void g2l_rowsq(uint16_t* tile, __amdgpu_buffer_rsrc_t rs, const RowsLaneQ& rl, int ld,
-                                          int row0, int m) {
-  __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_void_ptr)(tile + 512 * m), 16, (m & 1) ? rl.v1 : rl.v0,
-                                           (row0 + 8 * m) * ld * 2, 0, 0);
+                                          int row0, int m) {   // m: the part rl was made for
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_void_ptr)(tile + 512 * m), 16, rl.v, (row0 + 8 * m) * ld * 2, 0,
+                                           0);
 }
 // An operand of K step s of a product over the rows of a [32 rows][64] swzq tile Y (Y^T X, or X Y):
 // lane l gets column 32 db + l % 32 of the tile, rows 16s + 8(l / 32) + 0..7 in order, or with
@@ -795,7 +796,7 @@ __global__ __launch_bounds__(NTHREADS) void sel_carry64_kernel(
 
   const int q_ld = (int)qs.row;
   const __amdgpu_buffer_rsrc_t rs_q = rsrc(q0, (int64_t)Tq * q_ld * 2);   // rows past Tq read zero
-  const RowsLane rl_q(q_ld, lane);
+  const RowsLane rl_q(q_ld, lane, wave);
   const int nb = NBq - rb_lo;   // blocks walked; block rb_lo + t sits in buffer t mod NBUF
   g2l_rows64(sQ0, rs_q, rl_q, q_ld, rb_lo * TILE, wave);
   g2l_rows64(sQ1, rs_q, rl_q, q_ld, (rb_lo + 1) * TILE, wave);
@@ -1299,8 +1300,8 @@ __global__ __launch_bounds__(NTHREADS, G == 1 ? 3 : 2) void fwd64_kernel(
   // this wavefront's carry row (its query block's; keys past the end read zero)
   const __amdgpu_buffer_rsrc_t rs_c =
       rsrc(carry + ((int64_t)b * NBq + min(rb, NBq - 1)) * Tk, (int64_t)Tk * 4);
-  const RowsLane rl_k(k_ld, lane);
-  const RowsLaneQ rl_v(vs.row, lane);
+  const RowsLane rl_k(k_ld, lane, wave);
+  const RowsLaneQ rl_v(vs.row, lane, wave);
 
   // key tile kt's K and V rows (into B), and its head-0 K rows and carry rows (into S), by direct
   // loads only
@@ -2237,7 +2238,7 @@ __global__ __launch_bounds__(NTHREADS, 2) void bwd_kv64_kernel(
   const __amdgpu_buffer_rsrc_t rs_q0 = rsrc(view_head(q, qs, 0), (int64_t)T * q_ld * 2);
   const __amdgpu_buffer_rsrc_t rs_lse = rsrc(lse + (seq_row + hh) * ldt, ldt * 4);
   const __amdgpu_buffer_rsrc_t rs_ndb = rsrc(dbar + (seq_row + hh) * ldt, ldt * 4);
-  const RowsLaneQ rl_q(q_ld, lane), rl_do(do_ld, lane);
+  const RowsLaneQ rl_q(q_ld, lane, wave), rl_do(do_ld, lane, wave);
 
   // Everything query tile qb needs, into buffer B, by direct loads only (the tile loop holds no
   // register loads: the vector-memory counter drains in issue order, so waiting for one would wait
@@ -2812,7 +2813,7 @@ __global__ __launch_bounds__(DQ64_WAVES * 64, 1) void bwd_dq64_kernel(
   const __amdgpu_buffer_rsrc_t rs_c = rsrc(carry + ((int64_t)b * NB + qb_c) * T, (int64_t)T * 4);
   const __amdgpu_buffer_rsrc_t rs_u =
       rsrc(ucheck + ((int64_t)hh * nseq + b) * utri_floats(NB) + utri_row(qb_c), (int64_t)(qb_c + 1) * TILE * 4);
-  const RowsLaneQ rl_k(k_ld, lane), rl_v(v_ld, lane);
+  const RowsLaneQ rl_k(k_ld, lane, wave & 3), rl_v(v_ld, lane, wave & 3);
 
   // everything key tile ktile needs, into buffer B, by direct loads only (see bwd_kv64_kernel):
   // wavefronts 0-3 load a quarter of the K rows (and of head 0's), 4-7 of the V rows
