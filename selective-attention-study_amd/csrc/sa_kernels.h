@@ -366,6 +366,10 @@ __device__ __forceinline__ int swz32(int r, int c) { return r * 32 + ((c ^ ((r >
 __device__ __forceinline__ int swzq(int r, int c) { return r * 64 + ((c ^ (((r & 3) << 1) ^ ((r >> 2) & 3))) << 3); }
 
 typedef __attribute__((address_space(3))) void* lds_void_ptr;
+// The LDS address of a pointer into a __shared__ variable, as the address-space-3 pointer the direct
+// loads take: the low 32 bits of the generic address (a plain cast tests the pointer for null, a
+// compare and select on the scalar unit per load).
+__device__ __forceinline__ lds_void_ptr lds_ptr(const void* p) { return (lds_void_ptr)(uint32_t)(uintptr_t)p; }
 
 // A buffer resource over `bytes` bytes from p (loads past them read zero).
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t rsrc(const void* p, int64_t bytes) {
@@ -2244,15 +2248,18 @@ __global__ __launch_bounds__(NTHREADS, 2) void bwd_kv64_kernel(
   // register loads: the vector-memory counter drains in issue order, so waiting for one would wait
   // for the tiles behind it): part `wave` of each operand tile (each wavefront loads a quarter of
   // every tile), the row statistics (wavefronts 0, 1), and each wavefront's carry row of its keys
-  // (keys past the end read zero).
+  // (keys past the end read zero). Tiles load in order, last to first, so the carry row steps back
+  // one row per call.
+  const float* carry_row = carry_b + (int64_t)(NB - 1) * T;
   auto load_tile = [&](int qb, KvTileBuf64& B) {
     const int qbase = qb * TILE;
     if (wave == 0)
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(rs_lse, (lds_void_ptr)B.stat[0], 4, (lane & 31) * 4, qbase * 4, 0, 0);
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rs_lse, lds_ptr(B.stat[0]), 4, (lane & 31) * 4, qbase * 4, 0, 0);
     if (wave == 1)
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(rs_ndb, (lds_void_ptr)B.stat[1], 4, (lane & 31) * 4, qbase * 4, 0, 0);
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc(carry_b + (int64_t)qb * T, (int64_t)T * 4),
-                                             (lds_void_ptr)B.hist[wave], 4, j * 4, 0, 0, 0);
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rs_ndb, lds_ptr(B.stat[1]), 4, (lane & 31) * 4, qbase * 4, 0, 0);
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc(carry_row, (int64_t)T * 4), lds_ptr(B.hist[wave]), 4, j * 4, 0, 0,
+                                             0);
+    carry_row -= T;
     g2l_rowsq(B.r[0], rs_q, rl_q, q_ld, qbase, wave);
     g2l_rowsq(B.r[1], rs_do, rl_do, do_ld, qbase, wave);
     if (!has_h0) g2l_rowsq(B.r[2], rs_q0, rl_q, q_ld, qbase, wave);
@@ -2293,6 +2300,8 @@ __global__ __launch_bounds__(NTHREADS, 2) void bwd_kv64_kernel(
   // the tile loop in two instances, for head 0's workgroups and the others (see bwd_kv_kernel)
   auto sweep = [&](auto h0_tag) {
     constexpr bool H0 = decltype(h0_tag)::value;
+    // the checkpoint row of tile t's query block (the rows lie end to end, tiles run last to first)
+    float* urow = uplane + utri_row(NB - 1);
     // tile t (buffer t mod 2, named by ODD)
     auto tile_step = [&](int t, auto interior_tag, auto odd_tag) {
       constexpr bool INTERIOR = decltype(interior_tag)::value;
@@ -2303,7 +2312,7 @@ __global__ __launch_bounds__(NTHREADS, 2) void bwd_kv64_kernel(
       const bool more = t + 1 < ntiles;
       if (more) load_tile(qb - 1, ODD ? sB0 : sB1);   // into the other buffer, free since the last barrier
       if (INTERIOR || qbase + TILE - 1 >= key0) {   // else every query of the tile precedes every key
-        if (h == 0 && j < T) uplane[utri_row(qb) + j] = ucarry;   // j < (qb + 1) * TILE here
+        if (h == 0 && j < T) urow[j] = ucarry;   // j < (qb + 1) * TILE here
         const bool edge = !INTERIOR && ((qbase <= key0 + TILE - 1) || key0 < exempt);
         const bool split = !INTERIOR && split_keys;
         const TileMasks mk(j, qbase, T, exempt, h);
@@ -2345,6 +2354,7 @@ __global__ __launch_bounds__(NTHREADS, 2) void bwd_kv64_kernel(
         };
         body();
       }
+      urow -= 32 * qb;   // utri_row(qb - 1)
       wait_loads();
       __syncthreads();   // the next tile's operands are in; every wavefront is done with this one
     };
