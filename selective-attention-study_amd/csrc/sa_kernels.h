@@ -402,7 +402,7 @@ __device__ __forceinline__ int cols_lane(int64_t ld, int lane) {
 }
 __device__ __forceinline__ void g2l_rows64(uint16_t* tile, __amdgpu_buffer_rsrc_t rs, const RowsLane& rl, int ld,
                                            int row0, int m) {   // m: the part rl was made for
-  __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, lds_ptr(tile + 512 * m), 16, rl.v, (row0 + 8 * m) * ld * 2, 0,
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_void_ptr)(tile + 512 * m), 16, rl.v, (row0 + 8 * m) * ld * 2, 0,
                                            0);
 }
 //   rowsq: a [32 rows][64] tile in swzq layout, as rows64. Slot 64m + l holds row r = 8m + l/8,
@@ -417,7 +417,7 @@ struct RowsLaneQ {
 };
 __device__ __forceinline__ void g2l_rowsq(uint16_t* tile, __amdgpu_buffer_rsrc_t rs, const RowsLaneQ& rl, int ld,
                                           int row0, int m) {   // m: the part rl was made for
-  __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, lds_ptr(tile + 512 * m), 16, rl.v, (row0 + 8 * m) * ld * 2, 0,
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_void_ptr)(tile + 512 * m), 16, rl.v, (row0 + 8 * m) * ld * 2, 0,
                                            0);
 }
 // An operand of K step s of a product over the rows of a [32 rows][64] swzq tile Y (Y^T X, or X Y):
@@ -448,7 +448,7 @@ __device__ __forceinline__ bf16x8 get_trq(const uint16_t* t, int lane, int db, i
 }
 __device__ __forceinline__ void g2l_cols32(uint16_t* tile, __amdgpu_buffer_rsrc_t rs, int vl, int ld, int col0,
                                            int m) {
-  __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, lds_ptr(tile + 512 * m), 16, vl, (16 * m * ld + col0) * 2, 0,
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_void_ptr)(tile + 512 * m), 16, vl, (16 * m * ld + col0) * 2, 0,
                                            0);
 }
 // the wavefront's outstanding vector-memory operations (the direct loads included) have completed
@@ -1321,7 +1321,7 @@ __global__ __launch_bounds__(NTHREADS, G == 1 ? 3 : 2) void fwd64_kernel(
   auto load_sel = [&](int kt, FwdSelBuf64& S) {
     const int kbase = kt * TILE;
     g2l_rows64(S.k0, rs_kh, rl_k, k_ld, kbase, wave);
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(rs_c, lds_ptr(S.c[wave]), 4, (kbase + n) * 4, 0, 0, 0);
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(rs_c, (lds_void_ptr)S.c[wave], 4, (kbase + n) * 4, 0, 0, 0);
   };
   auto rfrag = [&](const elem* tile, int s) -> frag {
     return *reinterpret_cast<const frag*>(tile + swz64(n, 2 * s + h));
@@ -2837,8 +2837,8 @@ __global__ __launch_bounds__(DQ64_WAVES * 64, 1) void bwd_dq64_kernel(
       g2l_rowsq(B.v, rs_v, rl_v, v_ld, kbase, m);
     }
     const int jo = (kbase + n) * 4;
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(rs_c, lds_ptr(B.hist[wave]), 4, jo, 0, 0, 0);
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(rs_u, lds_ptr(B.uin[wave]), 4, jo, 0, 0, 0);
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(rs_c, (lds_void_ptr)B.hist[wave], 4, jo, 0, 0, 0);
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(rs_u, (lds_void_ptr)B.uin[wave], 4, jo, 0, 0, 0);
   };
   // fragment s of row n (lane = key) of a swzq tile
   auto rfrag = [&](const elem* tile, int s) -> frag {
