@@ -351,11 +351,6 @@ __device__ __forceinline__ BlockXY xcd_block() {
 // (measured: a rotation by r or an XOR by r mod 8 takes twice the cycles).
 __device__ __forceinline__ int swz64(int r, int c) { return r * 64 + (((c + (r >> 1)) & 7) << 3); }
 
-// Unpadded LDS rows of 32 bf16 (four 16-byte chunks), chunk c of row r stored at chunk
-// c ^ ((r / 4) mod 4): a 16-byte read of one chunk by 16 consecutive rows (16 lanes per pass over
-// 64 four-byte banks) touches 16 distinct bank groups.
-__device__ __forceinline__ int swz32(int r, int c) { return r * 32 + ((c ^ ((r >> 2) & 3)) << 3); }
-
 // Unpadded LDS rows of 64 bf16 read both ways: by lane-per-row fragment reads and by transposing
 // reads (get_trq). Chunk c of row r is stored at chunk c ^ f(r), f(r) = 2 (r mod 4) ^ (r/4 mod 4).
 // A 16-byte read of one chunk by 16 consecutive rows (16 lanes per pass over 64 four-byte banks):
@@ -366,10 +361,6 @@ __device__ __forceinline__ int swz32(int r, int c) { return r * 32 + ((c ^ ((r >
 __device__ __forceinline__ int swzq(int r, int c) { return r * 64 + ((c ^ (((r & 3) << 1) ^ ((r >> 2) & 3))) << 3); }
 
 typedef __attribute__((address_space(3))) void* lds_void_ptr;
-// The LDS address of a pointer into a __shared__ variable, as the address-space-3 pointer the direct
-// loads take: the low 32 bits of the generic address (a plain cast tests the pointer for null, a
-// compare and select on the scalar unit per load).
-__device__ __forceinline__ lds_void_ptr lds_ptr(const void* p) { return (lds_void_ptr)(uint32_t)(uintptr_t)p; }
 
 // A buffer resource over `bytes` bytes from p (loads past them read zero).
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t rsrc(const void* p, int64_t bytes) {
@@ -379,14 +370,11 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t rsrc(const void* p, int64_t by
 // Direct loads into LDS: one instruction fills 64 consecutive 16-byte slots (1 KB) from the given
 // LDS base, lane l slot l (measured lane layout on gfx950); each lane reads the global chunk that
 // belongs in its slot, through a buffer resource (the scalar offset counts in the range check,
-// measured: rows past the resource load zero). A [32][64] or [64][32] bf16 tile takes four such
-// loads, parts m = 0..3.
+// measured: rows past the resource load zero). A [32][64] bf16 tile takes four such loads, parts
+// m = 0..3.
 //   rows64: a [32 rows][64] tile in swz64 layout from rows row0.. of a row-major matrix (row stride
 //           ld elements). Slot 64m + l holds row 8m + l/8, stored chunk l mod 8, so logical chunk
 //           (l mod 8 - l/16 - 4m) mod 8: c0 = (l mod 8 - l/16) mod 8 for even m, c0 ^ 4 for odd m.
-//   cols32: a [64 rows][32] tile in swz32 layout, columns col0.. of one of this library's transposed
-//           copies (row stride ld, zero-filled past T). Slot 64m + l holds row 16m + l/4, logical
-//           chunk (l mod 4) ^ (l/16 mod 4).
 // A wavefront always loads the same part m of every tile, so the lane's offset is chosen once, as a
 // value (a per-load choice between two fields compiled into a choice of addresses, which kept the
 // pair in scratch memory and made every load wait for a scratch read first).
@@ -397,9 +385,6 @@ struct RowsLane {
     v = ((lane >> 3) * ld + 8 * ((m & 1) ? (c0 ^ 4) : c0)) * 2;
   }
 };
-__device__ __forceinline__ int cols_lane(int64_t ld, int lane) {
-  return (int)((lane >> 2) * ld + 8 * ((lane & 3) ^ ((lane >> 4) & 3))) * 2;
-}
 __device__ __forceinline__ void g2l_rows64(uint16_t* tile, __amdgpu_buffer_rsrc_t rs, const RowsLane& rl, int ld,
                                            int row0, int m) {   // m: the part rl was made for
   __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_void_ptr)(tile + 512 * m), 16, rl.v, (row0 + 8 * m) * ld * 2, 0,
@@ -445,11 +430,6 @@ __device__ __forceinline__ bf16x8 get_trq(const uint16_t* t, int lane, int db, i
     }
   }
   return f;
-}
-__device__ __forceinline__ void g2l_cols32(uint16_t* tile, __amdgpu_buffer_rsrc_t rs, int vl, int ld, int col0,
-                                           int m) {
-  __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_void_ptr)(tile + 512 * m), 16, vl, (16 * m * ld + col0) * 2, 0,
-                                           0);
 }
 // the wavefront's outstanding vector-memory operations (the direct loads included) have completed
 __device__ __forceinline__ void wait_loads() { __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
@@ -1509,8 +1489,8 @@ __global__ __launch_bounds__(NTHREADS, G == 1 ? 3 : 2) void fwd64_kernel(
 
 // ---------------------------------------------------------------------------------------------
 // Backward preparation: lse = rmax + log2(rden), ndbar = -rowsum(dO * O) (negated: the dO.v
-// products accumulate onto it), and the transposed copies K^T and (except at bf16 head dim 64,
-// whose key-side kernel reads its Q, dO rows transposed from LDS) Q^T, dO^T (R, D, ldt). The
+// products accumulate onto it), and, except at bf16 head dim 64 (whose kernels read the rows
+// transposed from LDS), the transposed copies Q^T, dO^T, K^T (R, D, ldt). The
 // statistics are laid out (R, ldt), each head's rows padded to ldt with lse = +inf (P = 0) and
 // ndbar = 0, so a 32-row tile of them is always in bounds; they take D/8 lanes per row (8 elements
 // each, so the loads of a row are contiguous across its lanes); transposes go by tiles.
@@ -2234,8 +2214,8 @@ __global__ __launch_bounds__(NTHREADS, 2) void bwd_kv64_kernel(
   const int qb_lo = bxy.x * NWAVES;
   const int ntiles = NB - qb_lo;
 
-  // operand sources (buffer resources over one head's rows, or its transposed copy) and this
-  // lane's parts of the direct loads
+  // operand sources (buffer resources over one head's rows) and this lane's parts of the direct
+  // loads
   const int q_ld = view_ld(qs), do_ld = view_ld(dos);
   const __amdgpu_buffer_rsrc_t rs_q = rsrc(view_head(q, qs, hh), (int64_t)T * q_ld * 2);
   const __amdgpu_buffer_rsrc_t rs_do = rsrc(view_head(dout, dos, hh), (int64_t)T * do_ld * 2);
@@ -2254,10 +2234,10 @@ __global__ __launch_bounds__(NTHREADS, 2) void bwd_kv64_kernel(
   auto load_tile = [&](int qb, KvTileBuf64& B) {
     const int qbase = qb * TILE;
     if (wave == 0)
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(rs_lse, lds_ptr(B.stat[0]), 4, (lane & 31) * 4, qbase * 4, 0, 0);
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rs_lse, (lds_void_ptr)B.stat[0], 4, (lane & 31) * 4, qbase * 4, 0, 0);
     if (wave == 1)
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(rs_ndb, lds_ptr(B.stat[1]), 4, (lane & 31) * 4, qbase * 4, 0, 0);
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc(carry_row, (int64_t)T * 4), lds_ptr(B.hist[wave]), 4, j * 4, 0, 0,
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rs_ndb, (lds_void_ptr)B.stat[1], 4, (lane & 31) * 4, qbase * 4, 0, 0);
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc(carry_row, (int64_t)T * 4), (lds_void_ptr)B.hist[wave], 4, j * 4, 0, 0,
                                              0);
     carry_row -= T;
     g2l_rowsq(B.r[0], rs_q, rl_q, q_ld, qbase, wave);
@@ -2814,8 +2794,8 @@ __global__ __launch_bounds__(DQ64_WAVES * 64, 1) void bwd_dq64_kernel(
   const float sl2 = scale * LOG2E;
   const float neg_inv_scale = -1.f / scale;
 
-  // key-side sources (buffer resources over one head's rows, or its transposed copy), this
-  // wavefront's rows of the carry and of the U checkpoints (keys past them read zero)
+  // key-side sources (buffer resources over one head's rows), this wavefront's rows of the carry
+  // and of the U checkpoints (keys past them read zero)
   const int k_ld = view_ld(ks), v_ld = view_ld(vs);
   const __amdgpu_buffer_rsrc_t rs_k = rsrc(view_head(k, ks, hh), (int64_t)T * k_ld * 2);
   const __amdgpu_buffer_rsrc_t rs_k0 = rsrc(view_head(k, ks, 0), (int64_t)T * k_ld * 2);
