@@ -2,8 +2,10 @@
 element from one wavefront in a fixed order (the only atomics are the per-head-group adds of head
 0's dQ / dK shares, summed in fp32 from zeroed targets, which the multi-head checks below leave out
 of the bitwise comparison), so any difference between two runs is a race -- an LDS buffer read
-before its direct load landed, or overwritten while still read. The reference's Triton kernels are
-deterministic the same way (one program per output tile).
+before its direct load landed, or overwritten while still read. The reference's backward is not
+deterministic in this sense: it adds dQ per key block with relaxed fp32 atomics
+(src/selective_attention/kernels.py:257, 283), where this build's query side owns each dQ row and
+stores it once.
 
 The shapes put every kernel instance of the bf16 head-dim-64 path to work: two heads per wavefront
 in the forward and the multi-head backward kernels (B=1, H=4, T=2048), one head per wavefront with
