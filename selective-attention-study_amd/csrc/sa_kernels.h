@@ -1441,6 +1441,9 @@ __global__ __launch_bounds__(NTHREADS, G == 1 ? 3 : 2) void fwd64_kernel(
   const int i_hi = max(i_lo, min(min(q_off + qsb * NWAVES * TILE, Tk) / TILE, wg_end));
   auto sweep = [&](auto damp_tag) {
     if (wg_end - 1 < my_end) select(wg_end - 1, sS0, damp_tag);   // the first tile's F
+    // The first tile step loads tile 2's head-0 K rows into sS0, whose rows every wavefront has
+    // just read for that F: all of them must be past their reads first.
+    __syncthreads();
     auto run = [&](int t0, int t1, auto interior_tag) {
       int t = t0;
       if (t < t1 && (t & 1)) tile_step(t++, interior_tag, damp_tag, std::true_type{});
