@@ -361,6 +361,10 @@ __device__ __forceinline__ int swz64(int r, int c) { return r * 64 + (((c + (r >
 __device__ __forceinline__ int swzq(int r, int c) { return r * 64 + ((c ^ (((r & 3) << 1) ^ ((r >> 2) & 3))) << 3); }
 
 typedef __attribute__((address_space(3))) void* lds_void_ptr;
+// The LDS address of a pointer into a __shared__ variable, as the address-space-3 pointer the direct
+// loads take: the low 32 bits of the generic address (a plain cast tests the pointer for null, a
+// compare and select on the scalar unit per load).
+__device__ __forceinline__ lds_void_ptr lds_ptr(const void* p) { return (lds_void_ptr)(uint32_t)(uintptr_t)p; }
 
 // A buffer resource over `bytes` bytes from p (loads past them read zero).
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t rsrc(const void* p, int64_t bytes) {
@@ -387,7 +391,7 @@ struct RowsLane {
 };
 __device__ __forceinline__ void g2l_rows64(uint16_t* tile, __amdgpu_buffer_rsrc_t rs, const RowsLane& rl, int ld,
                                            int row0, int m) {   // m: the part rl was made for
-  __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_void_ptr)(tile + 512 * m), 16, rl.v, (row0 + 8 * m) * ld * 2, 0,
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, lds_ptr(tile + 512 * m), 16, rl.v, (row0 + 8 * m) * ld * 2, 0,
                                            0);
 }
 //   rowsq: a [32 rows][64] tile in swzq layout, as rows64. Slot 64m + l holds row r = 8m + l/8,
@@ -402,7 +406,7 @@ struct RowsLaneQ {
 };
 __device__ __forceinline__ void g2l_rowsq(uint16_t* tile, __amdgpu_buffer_rsrc_t rs, const RowsLaneQ& rl, int ld,
                                           int row0, int m) {   // m: the part rl was made for
-  __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_void_ptr)(tile + 512 * m), 16, rl.v, (row0 + 8 * m) * ld * 2, 0,
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, lds_ptr(tile + 512 * m), 16, rl.v, (row0 + 8 * m) * ld * 2, 0,
                                            0);
 }
 // An operand of K step s of a product over the rows of a [32 rows][64] swzq tile Y (Y^T X, or X Y):
@@ -1301,7 +1305,7 @@ __global__ __launch_bounds__(NTHREADS, G == 1 ? 3 : 2) void fwd64_kernel(
   auto load_sel = [&](int kt, FwdSelBuf64& S) {
     const int kbase = kt * TILE;
     g2l_rows64(S.k0, rs_kh, rl_k, k_ld, kbase, wave);
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(rs_c, (lds_void_ptr)S.c[wave], 4, (kbase + n) * 4, 0, 0, 0);
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(rs_c, lds_ptr(S.c[wave]), 4, (kbase + n) * 4, 0, 0, 0);
   };
   auto rfrag = [&](const elem* tile, int s) -> frag {
     return *reinterpret_cast<const frag*>(tile + swz64(n, 2 * s + h));
@@ -2237,10 +2241,10 @@ __global__ __launch_bounds__(NTHREADS, 2) void bwd_kv64_kernel(
   auto load_tile = [&](int qb, KvTileBuf64& B) {
     const int qbase = qb * TILE;
     if (wave == 0)
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(rs_lse, (lds_void_ptr)B.stat[0], 4, (lane & 31) * 4, qbase * 4, 0, 0);
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rs_lse, lds_ptr(B.stat[0]), 4, (lane & 31) * 4, qbase * 4, 0, 0);
     if (wave == 1)
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(rs_ndb, (lds_void_ptr)B.stat[1], 4, (lane & 31) * 4, qbase * 4, 0, 0);
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc(carry_row, (int64_t)T * 4), (lds_void_ptr)B.hist[wave], 4, j * 4, 0, 0,
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rs_ndb, lds_ptr(B.stat[1]), 4, (lane & 31) * 4, qbase * 4, 0, 0);
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc(carry_row, (int64_t)T * 4), lds_ptr(B.hist[wave]), 4, j * 4, 0, 0,
                                              0);
     carry_row -= T;
     g2l_rowsq(B.r[0], rs_q, rl_q, q_ld, qbase, wave);
@@ -2820,8 +2824,8 @@ __global__ __launch_bounds__(DQ64_WAVES * 64, 1) void bwd_dq64_kernel(
       g2l_rowsq(B.v, rs_v, rl_v, v_ld, kbase, m);
     }
     const int jo = (kbase + n) * 4;
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(rs_c, (lds_void_ptr)B.hist[wave], 4, jo, 0, 0, 0);
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(rs_u, (lds_void_ptr)B.uin[wave], 4, jo, 0, 0, 0);
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(rs_c, lds_ptr(B.hist[wave]), 4, jo, 0, 0, 0);
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(rs_u, lds_ptr(B.uin[wave]), 4, jo, 0, 0, 0);
   };
   // fragment s of row n (lane = key) of a swzq tile
   auto rfrag = [&](const elem* tile, int s) -> frag {
