@@ -47,13 +47,13 @@ KERNEL_FLOP = {"forward": 2.0 * UNIT, "backward_kv": 4.0 * UNIT, "backward_dq": 
 # WRITE_SIZE counters (one pass each) and scaled by a 1 GiB copy's readings (FETCH x 2.0, WRITE x
 # 1.0): profiles/c2_attention_kernels_traffic.md. The counters need the profiler, so bench.py
 # reports the committed measurement; re-measure after a kernel change.
-MEASURED_TRAFFIC_BYTES = {"forward": (2.0 * 424_212 + 67_586) * 1024,
-                          "backward_kv": (2.0 * 347_176 + 582_303) * 1024,
-                          "backward_dq": (2.0 * 447_655 + 96_256) * 1024}
+MEASURED_TRAFFIC_BYTES = {"forward": (2.0 * 492_964 + 67_585) * 1024,
+                          "backward_kv": (2.0 * 348_650 + 582_272) * 1024,
+                          "backward_dq": (2.0 * 446_130 + 96_256) * 1024}
 # C4 (131072-token prefill, 8 chunks): the forward kernel's HBM bytes per launch (mean over the
 # chunks, FETCH_SIZE x 2.0 + WRITE_SIZE x 1.0) and MFMA busy fraction, measured with rocprofv3:
 # profiles/c4_prefill_kernels.md. The run's own per-launch time turns the bytes into a rate.
-MEASURED_C4 = {"hbm_bytes_per_launch": (2.0 * 3_264_747 + 67_584) * 1024, "mfma_busy": 0.35}
+MEASURED_C4 = {"hbm_bytes_per_launch": (2.0 * 3_702_120 + 67_584) * 1024, "mfma_busy": 0.35}
 
 
 def _cpu_model() -> str:
