@@ -148,7 +148,7 @@ def main() -> int:
     args = ap.parse_args()
     if args.gpus != 1:
         print("bench.py measures one GPU only: the operator runs on a single MI355X "
-              "(multi-GPU sharding is described in DESIGN.md, not run)", file=sys.stderr)
+              "(sharding across GPUs is a design here, not a code path)", file=sys.stderr)
         return 2
 
     import torch
