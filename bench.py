@@ -18,8 +18,11 @@ The same line carries BASELINE's other configurations (selective_attention/harne
           (the reference's 209M d768 / 12 heads, and BASELINE's literal d1024 / 16 heads)
   c4      C4, the 131072-token prefill in 8 chunks of 16384 through 24 d1024 layers
   c5      C5, per-head selection fwd+bwd at B=2 H=16 T=32768 D=64 with its dominant kernel's roofline
+  reference_shapes  one layer's fwd and bwd at the reference's own published shapes (B=2 H=12 D=64,
+          T = 2K ... 16K), timed as its scripts/bench_kernels.py does, beside its published figures
+          (other hardware: context, not a target)
 
-    python bench.py [--steps K] [--warmup W] [--no-cpu-baseline] [--no-train] [--no-configs]
+    python bench.py [--steps K] [--warmup W] [--no-cpu-baseline] [--no-train] [--no-configs] [--no-ref-shapes]
 """
 
 from __future__ import annotations
@@ -46,7 +49,8 @@ KERNEL_FLOP = {"forward": 2.0 * UNIT, "backward_kv": 4.0 * UNIT, "backward_dq": 
 # HBM bytes per launch of each kernel at this workload, measured with rocprofv3's FETCH_SIZE and
 # WRITE_SIZE counters (one pass each) and scaled by a 1 GiB copy's readings (FETCH x 2.0, WRITE x
 # 1.0): profiles/c2_attention_kernels_traffic.md. The counters need the profiler, so bench.py
-# reports the committed measurement; re-measure after a kernel change.
+# reports the committed measurement, labelled with the hash of the kernel sources it was taken on
+# (PROFILED_SOURCES): the line says whether the sources it runs are still those.
 MEASURED_TRAFFIC_BYTES = {"forward": (2.0 * 492_964 + 67_585) * 1024,
                           "backward_kv": (2.0 * 348_650 + 582_272) * 1024,
                           "backward_dq": (2.0 * 446_130 + 96_256) * 1024}
@@ -54,6 +58,23 @@ MEASURED_TRAFFIC_BYTES = {"forward": (2.0 * 492_964 + 67_585) * 1024,
 # chunks, FETCH_SIZE x 2.0 + WRITE_SIZE x 1.0) and MFMA busy fraction, measured with rocprofv3:
 # profiles/c4_prefill_kernels.md. The run's own per-launch time turns the bytes into a rate.
 MEASURED_C4 = {"hbm_bytes_per_launch": (2.0 * 3_702_120 + 67_584) * 1024, "mfma_busy": 0.35}
+# sha256 (first 16 hex digits) of csrc/sa_kernels.h when the figures above were profiled
+PROFILED_SOURCES = "65cbbc894ea490ba"
+KERNEL_SOURCE = os.path.join(ROOT, "selective-attention-study_amd", "csrc", "sa_kernels.h")
+
+
+def _profiled_label() -> dict:
+    """Where the committed counter figures come from, and whether this run's kernels are the ones
+    they were taken on (the kernel source's hash against the one recorded with them)."""
+    import hashlib
+
+    try:
+        with open(KERNEL_SOURCE, "rb") as f:
+            now = hashlib.sha256(f.read()).hexdigest()[:16]
+    except OSError:
+        now = None
+    return {"profiled_sources_sha16": PROFILED_SOURCES, "current_sources_sha16": now,
+            "current": now == PROFILED_SOURCES}
 
 
 def _cpu_model() -> str:
@@ -145,6 +166,8 @@ def main() -> int:
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-train", action="store_true", help="skip the 24-layer training-step rates (C3)")
     ap.add_argument("--no-configs", action="store_true", help="skip the C4 prefill and C5 per-head rates")
+    ap.add_argument("--no-ref-shapes", action="store_true",
+                    help="skip the one-layer timings at the reference's published shapes (B=2 H=12)")
     args = ap.parse_args()
     if args.gpus != 1:
         print("bench.py measures one GPU only: the operator runs on a single MI355X "
@@ -169,6 +192,7 @@ def main() -> int:
         out = kernels.selective_attention(q, k, v)
         return torch.autograd.grad(out, (q, k, v), do)
 
+    torch.cuda.reset_peak_memory_stats()
     for _ in range(args.warmup):
         step()
     torch.cuda.synchronize()
@@ -182,6 +206,7 @@ def main() -> int:
     stop.record()
     torch.cuda.synchronize()
     ms = start.elapsed_time(stop) / args.steps
+    peak_gib = torch.cuda.max_memory_allocated() / 2**30
     per_kernel = {}
     for name, kid in (("forward", _lib.KERNEL_FORWARD), ("backward_kv", _lib.KERNEL_BACKWARD),
                       ("backward_dq", _lib.KERNEL_BACKWARD_DQ), ("selection", _lib.KERNEL_SELECTION)):
@@ -210,11 +235,13 @@ def main() -> int:
                    "flop_per_step": STEP_FLOP, "flop_convention": "7*B*H*D*T^2 (fwd 2, bwd 5; causal T^2/2)"},
         "frac_of_peak": round(tflops / PEAK_BF16_TFLOPS, 4),
         "kernel_ms": {k_: round(v_, 4) for k_, v_ in per_kernel.items()},
+        "peak_mem_gib": round(peak_gib, 4),
         "roofline": {"bound": "mfma",
                      "kernel": f"{dominant} ({KERNEL_FLOP[dominant] / UNIT:.0f}*B*H*D*T^2 FLOP per launch)",
                      "achieved": round(achieved, 2), "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
                      "frac": round(achieved / PEAK_BF16_TFLOPS, 4),
-                     "traffic": MEASURED_TRAFFIC_BYTES[dominant], "traffic_unit": "bytes per launch (rocprofv3)"},
+                     "traffic": MEASURED_TRAFFIC_BYTES[dominant], "traffic_unit": "bytes per launch (rocprofv3)",
+                     "traffic_source": dict(_profiled_label(), file="profiles/c2_attention_kernels_traffic.md")},
     }
     del q, k, v, do, grads
     torch.cuda.empty_cache()
@@ -233,7 +260,7 @@ def main() -> int:
         record["train_tok_s"] = round(record["train"]["d768"]["tokens_per_s"], 1)
     if not args.no_configs:
         c4 = harness.prefill_rate(reps=2, warmup=1)
-        c4["counters"] = {"source": "profiles/c4_prefill_kernels.md (rocprofv3 --pmc)",
+        c4["counters"] = {"source": dict(_profiled_label(), file="profiles/c4_prefill_kernels.md (rocprofv3 --pmc)"),
                           "mfma_busy": MEASURED_C4["mfma_busy"],
                           "hbm_bytes_per_launch": MEASURED_C4["hbm_bytes_per_launch"],
                           "hbm_tb_s": MEASURED_C4["hbm_bytes_per_launch"] / (c4["per_layer_chunk_forward_ms"] * 1e9),
@@ -245,6 +272,11 @@ def main() -> int:
         record["c5"] = _rounded(harness.perhead_rate(steps=5, warmup=2))
         torch.cuda.empty_cache()
         _progress(f"C5 {record['c5']['ms_per_step']:.2f} ms/step")
+    if not args.no_ref_shapes:
+        record["reference_shapes"] = _rounded(harness.reference_shapes())
+        torch.cuda.empty_cache()
+        _progress("reference shapes " + ", ".join(f"T={t_}: {r_['total_ms']:.2f} ms"
+                                                  for t_, r_ in record["reference_shapes"]["by_seq"].items()))
     if not args.no_cpu_baseline:
         record["cpu_baseline"] = cpu_baseline()
         record["cpu_c1"] = _rounded(cpu_c1())

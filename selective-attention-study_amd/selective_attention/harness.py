@@ -157,7 +157,10 @@ def perhead_rate(batch: int = 2, heads: int = 16, seq: int = 32768, head_dim: in
         out = kernels.selective_attention(qq, kk, vv)
         torch.autograd.grad(out, (qq, kk, vv), dd)
 
+    torch.cuda.synchronize()
+    torch.cuda.reset_peak_memory_stats()
     ms = _timed(step, steps, warmup)
+    peak = torch.cuda.max_memory_allocated() / 2**30
     kernel_ms = kernel_times(step, steps)
     unit = batch * heads * head_dim * seq * seq   # one causal product over all heads
     flop = 7.0 * unit
@@ -166,10 +169,69 @@ def perhead_rate(batch: int = 2, heads: int = 16, seq: int = 32768, head_dim: in
     achieved = KERNEL_PRODUCTS[dominant] * unit / (kernel_ms[dominant] * 1e-3) / 1e12
     return {"config": f"C5 per-head fwd+bwd, B={batch} H={heads} T={seq} D={head_dim} bf16, k x2 on 10% of keys",
             "ms_per_step": ms, "tflops": tf, "frac_of_peak": tf / PEAK_BF16_TFLOPS,
-            "kernel_ms": kernel_ms,
+            "kernel_ms": kernel_ms, "peak_mem_gib": peak,
             "roofline": {"bound": "mfma", "kernel": f"{dominant} ({KERNEL_PRODUCTS[dominant]:.0f}*B*H*D*T^2 FLOP)",
                          "achieved": achieved, "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
                          "frac": achieved / PEAK_BF16_TFLOPS}}
+
+
+# The reference's published one-layer figures (results/bench/layer_fwd_bwd_v2.json:26-93, op
+# "selective", B=2 H=12 D=64 bf16, 20 reps on an NVIDIA RTX PRO 6000 Blackwell): seq -> (fwd ms,
+# bwd ms, peak GiB). Different hardware: context for the same measurement here, not a target.
+REFERENCE_PUBLISHED = {2048: (0.3402, 0.8208, 0.0914), 4096: (0.6385, 1.6529, 0.1847),
+                       8192: (1.8703, 5.2663, 0.3772), 16384: (6.4977, 21.1941, 0.7856)}
+
+
+def reference_shapes(seqs=(2048, 4096, 8192, 16384), batch: int = 2, heads: int = 12, head_dim: int = 64,
+                     reps: int = 20) -> dict:
+    """One attention layer's forward and backward timed as the reference's scripts/bench_kernels.py:30-59
+    times them: bf16 q, k, v ~ N(0,1) (torch.manual_seed(0)) and a bf16 weight; the forward, a
+    synchronize, then (out.to(bf16) * weight).sum().backward() and a synchronize, host clock around
+    each half, 3 warm-ups and the mean of `reps`; peak memory is the allocator's high-water mark over
+    the timed steps, inputs included."""
+    import time
+
+    rows = {}
+    for seq in seqs:
+        torch.manual_seed(0)
+        q, k, v = (torch.randn(batch, heads, seq, head_dim, device="cuda", dtype=torch.bfloat16, requires_grad=True)
+                   for _ in range(3))
+        weight = torch.randn(batch, heads, seq, head_dim, device="cuda", dtype=torch.bfloat16)
+
+        def step():
+            out = kernels.selective_attention(q, k, v, dot_precision="bf16")
+            torch.cuda.synchronize()
+            mid = time.perf_counter()
+            (out.to(weight.dtype) * weight).sum().backward()
+            torch.cuda.synchronize()
+            q.grad = k.grad = v.grad = None
+            return mid
+
+        for _ in range(3):
+            step()
+        torch.cuda.reset_peak_memory_stats()
+        fwd = bwd = 0.0
+        for _ in range(reps):
+            torch.cuda.synchronize()
+            start = time.perf_counter()
+            mid = step()
+            end = time.perf_counter()
+            fwd += mid - start
+            bwd += end - mid
+        fwd_ms, bwd_ms = 1e3 * fwd / reps, 1e3 * bwd / reps
+        row = {"fwd_ms": fwd_ms, "bwd_ms": bwd_ms, "total_ms": fwd_ms + bwd_ms,
+               "peak_gib": torch.cuda.max_memory_allocated() / 2**30,
+               "tflops": 7.0 * batch * heads * head_dim * seq * seq / ((fwd_ms + bwd_ms) * 1e-3) / 1e12}
+        if seq in REFERENCE_PUBLISHED:
+            rf, rb, rp = REFERENCE_PUBLISHED[seq]
+            row["reference_published"] = {"fwd_ms": rf, "bwd_ms": rb, "total_ms": rf + rb, "peak_gib": rp}
+        rows[str(seq)] = row
+        del q, k, v, weight
+        torch.cuda.empty_cache()
+    return {"config": f"one layer fwd+bwd at the reference's published shapes: B={batch} H={heads} D={head_dim} bf16, "
+                      f"timed as scripts/bench_kernels.py (host clock per half, {reps} reps)",
+            "reference_source": "results/bench/layer_fwd_bwd_v2.json:26-93 (RTX PRO 6000 Blackwell; context only)",
+            "by_seq": rows}
 
 
 # Products each timed kernel computes (recomputation included), in units of one causal product over

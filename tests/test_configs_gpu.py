@@ -4,8 +4,12 @@ tensors (reference tests/test_selective_kernels.py:310-345, tests/test_selective
   C4  one attention layer's prefill of 131,072 tokens in 8 chunks of 16,384 (B=1, H=16, D=64,
       bf16): chunked == single shot, the last 1000 queries against the oracle's chunk-summed tail form,
       the carried per-key state against the tail's totals
-  C3  one training step of the 24-layer d1024 / 16-head decoder at 1 x 16,384 tokens under bf16
-      autocast: finite loss and gradients; chunked model prefill == single-shot prefill
+  C5  per-head selection fwd+bwd at B=2, H=16, T=32,768, D=64 in bf16 on the bench's own inputs: the
+      first 2048 rows == a T=2048 run bit for bit, the last rows of two sequences against the
+      oracle's tail, finite gradients, the last key's dV against P[T-1, T-1] dO[T-1]
+  C3  one training step of the 24-layer decoder at 1 x 16,384 tokens under bf16 autocast, at the
+      reference's d768 / 12-head geometry and BASELINE's d1024 / 16-head one: finite loss and
+      gradients; chunked model prefill == single-shot prefill
   the forward past the int32 offset limit (T = 270,000, where CARRY's block x T index passes 2^31)
 
 The oracle's tail runs in float64 on the GPU box's GPU here (plain torch products on the oracle's
@@ -82,14 +86,7 @@ def test_bf16_fwd_bwd_past_the_int32_offset_limit(cuda):
     print(f"tail max-abs {err:.2e}", flush=True)
     assert err < 2e-2
     assert all(torch.isfinite(x).all() for x in (dq, dk, dv))
-    # the last row's weight on its own key: its logits less the history every key gathered from the
-    # earlier queries (the totals less the last query's own selection)
-    qd, kd = q.detach().double(), k.detach().double()
-    lg = sa_oracle.raw_logits(qd[:, :, -1:], kd)                          # (1, H, 1, T)
-    own = sa_oracle.selection(qd[:, :, -1:], kd, 1, q_offset=seq - 1)     # (1, 1, T)
-    hist = total - own[:, 0]                                              # (1, T)
-    p = torch.softmax(lg - hist[:, None, None, :], dim=-1)[..., -1]       # (1, H, 1)
-    want_dv = p[..., None] * dout[:, :, -1:].double()
+    want_dv = _last_key_dv(q.detach().double(), k.detach().double(), dout, total)
     got_dv = dv[:, :, -1:].double()
     scale = want_dv.abs().max().item()
     rel = ((got_dv - want_dv).abs().max() / scale).item()
@@ -97,15 +94,80 @@ def test_bf16_fwd_bwd_past_the_int32_offset_limit(cuda):
     assert rel < 2e-2
 
 
-def test_c3_training_step_d1024_16384(cuda):
+def _last_key_dv(q, k, dout, total):
+    """dV of the last key, which only the last query attends: P[T-1, T-1] dO[T-1] per head, P the
+    last row's softmax over its logits less the history every key gathered from the earlier queries
+    (the totals less the last query's own selection). q, k (B, H, T, D) float64; total (B, T)."""
+    seq = q.shape[2]
+    lg = sa_oracle.raw_logits(q[:, :, -1:], k)                           # (B, H, 1, T)
+    own = sa_oracle.selection(q[:, :, -1:], k, 1, q_offset=seq - 1)      # (B, 1, T)
+    hist = total - own[:, 0]                                             # (B, T)
+    p = torch.softmax(lg - hist[:, None, None, :], dim=-1)[..., -1]      # (B, H, 1)
+    return p[..., None] * dout[:, :, -1:].double()
+
+
+def test_c5_per_head_full_size(cuda):
+    """C5 at its full size on the bench's own inputs (harness.perhead_rate: q, k, v, dO ~ N(0,1) from
+    seed 5 on the GPU, k scaled by 2 on a random 10% of key positions, each head its own one-head
+    sequence): the one-pass selection carry over 32 sequences (4.3 GB of CARRY), the one-head forward
+    and the one-head backward instances at T = 32768. The first 2048 output rows equal a T=2048 run
+    bit for bit (causality); the last 64 rows of two sequences and their selection totals agree with
+    the oracle's tail (float64 on the GPU); the gradients are finite and in bf16; the last key's dV
+    equals P[T-1, T-1] dO[T-1] (reference tests/test_selective_perhead.py:55-77 checks per-head
+    selection against each head alone, here at the configuration's own length)."""
+    b, h, t, d = 2, 16, 32768, 64
+    print(f"case C5 per-head full size B={b} H={h} T={t}", flush=True)
+    g = torch.Generator(device=cuda).manual_seed(5)
+    q, k, v, do = (torch.randn(b, h, t, d, device=cuda, generator=g) for _ in range(4))
+    boost = torch.rand(b, h, t, 1, device=cuda, generator=g) < 0.1
+    k = torch.where(boost, 2.0 * k, k)
+    r = lambda x: x.reshape(b * h, 1, t, d)
+    qq, kk, vv = (r(x).bfloat16() for x in (q, k, v))
+    dd = r(do)
+    del q, k, v, do, boost
+    full, aux = kernels.selective_attention_forward(qq, kk, vv, return_aux=True)
+    totals = aux["selected_total"]
+    del aux
+    part = kernels.selective_attention_forward(qq[:, :, :2048].contiguous(), kk[:, :, :2048].contiguous(),
+                                               vv[:, :, :2048].contiguous())
+    assert torch.equal(full[:, :, :2048], part)
+    picks = (0, b * h - 1)
+    oracle_totals = {}
+    for sq in picks:
+        sl = slice(sq, sq + 1)
+        rows, want, total = sa_oracle.tail(qq[sl].double(), kk[sl].double(), vv[sl].double(), 64, chunk=4096)
+        err = (full[sl][:, :, rows].double() - want).abs().max().item()
+        trel = ((totals[sl].double() - total).abs().max() / total.abs().max()).item()
+        print(f"C5 sequence {sq}: tail max-abs {err:.2e}, totals rel {trel:.2e}", flush=True)
+        assert err < 2e-2
+        assert trel < 1e-3
+        oracle_totals[sq] = total
+    qs, ks, vs = (x.clone().requires_grad_(True) for x in (qq, kk, vv))
+    out = kernels.selective_attention(qs, ks, vs)
+    assert torch.equal(out.detach(), full)
+    del full, part
+    dq, dk, dv = torch.autograd.grad(out, (qs, ks, vs), dd)
+    for x in (dq, dk, dv):
+        assert x.dtype == torch.bfloat16 and torch.isfinite(x).all()
+    for sq in picks:
+        sl = slice(sq, sq + 1)
+        want_dv = _last_key_dv(qq[sl].double(), kk[sl].double(), dd[sl], oracle_totals[sq])
+        got_dv = dv[sl][:, :, -1:].double()
+        rel = ((got_dv - want_dv).abs().max() / want_dv.abs().max()).item()
+        print(f"C5 sequence {sq}: last-key dV rel {rel:.2e}", flush=True)
+        assert rel < 2e-2
+
+
+@pytest.mark.parametrize("geometry,params", [("d768", 208_540_416), ("d1024", 353_502_208)])
+def test_c3_training_step_16384(cuda, geometry, params):
     """C3: one full training step (forward, backward, clipping, fused AdamW) of the 24-layer
-    d1024 / 16-head decoder on 1 x 16,384 tokens under bf16 autocast: the loss and every gradient
-    are finite, over two steps."""
-    print("case C3 train step d1024 T=16384", flush=True)
-    cfg = ModelConfig(n_layers=24, context_length=16384, **harness.GEOMETRIES["d1024"])
+    decoder on 1 x 16,384 tokens under bf16 autocast, at the reference's d768 / 12-head model and
+    BASELINE's d1024 / 16-head geometry: the loss and every gradient are finite, over two steps."""
+    print(f"case C3 train step {geometry} T=16384", flush=True)
+    cfg = ModelConfig(n_layers=24, context_length=16384, **harness.GEOMETRIES[geometry])
     torch.manual_seed(0)
     model = SelectiveLM(cfg).to(cuda).train()
-    assert model.num_parameters() == 353_502_208
+    assert model.num_parameters() == params
     opt = torch.optim.AdamW(model.parameters(), lr=6e-4, betas=(0.9, 0.95), eps=1e-8, weight_decay=0.1, fused=True)
     idx, tgt = harness.synthetic_batch(1, 16384, cuda)
     losses = []

@@ -59,11 +59,19 @@ def test_repeated_fwd_bwd_is_bit_identical(cuda, shape):
         assert torch.equal(first[3], again[3])   # dV: plain stores
         if multi_head:
             # head 0's dQ, dK sum the other heads' shares with atomics: compare the other heads'
-            # bitwise, head 0's to fp32 rounding of a reordered sum
+            # bitwise, head 0's to within one bf16 ulp of each element (a reordered fp32 sum, then
+            # rounded to bf16, lands on the same or a neighbouring bf16 value), plus the fp32
+            # reordering noise of the tensor's largest terms (2^-20 of its largest value) where the
+            # shares cancel; a race on head 0's own path would move whole terms
             assert torch.equal(first[1][:, 1:], again[1][:, 1:])
             assert torch.equal(first[2][:, 1:], again[2][:, 1:])
-            torch.testing.assert_close(first[1][:, :1].float(), again[1][:, :1].float(), rtol=2e-2, atol=1e-3)
-            torch.testing.assert_close(first[2][:, :1].float(), again[2][:, :1].float(), rtol=2e-2, atol=1e-3)
+            for a, b in ((first[1][:, :1], again[1][:, :1]), (first[2][:, :1], again[2][:, :1])):
+                assert a.dtype == torch.bfloat16
+                a, b = a.float(), b.float()
+                _, e = torch.frexp(torch.maximum(a.abs(), b.abs()))
+                ulp = torch.ldexp(torch.ones_like(a), e - 8)   # bf16: 8 significant bits
+                bound = ulp + a.abs().max() * 2.0 ** -20
+                assert ((a - b).abs() <= bound).all(), ((a - b).abs() / bound).max().item()
         else:
             assert torch.equal(first[1], again[1])
             assert torch.equal(first[2], again[2])
