@@ -737,7 +737,19 @@ __global__ __launch_bounds__(NTHREADS) void sel_carry64_kernel(
   constexpr int D = 64, NS = 4, KPW = SEL_CARRY_KPW, NBUF = SEL_CARRY_NBUF, AHEAD = NBUF - 1;
   static_assert(NBUF == 4, "the block loop names four buffers");
   // separate LDS variables, named at compile time, so the compiler knows a block's reads do not
-  // touch the buffers the direct loads are filling
+  // touch the buffers the direct loads are filling.
+  // Lifetimes (block rb_lo + t lives in buffer t mod 4):
+  //   filled: by the direct load g2l_rows64 of every wavefront (a quarter each), for blocks rb_lo,
+  //           +1, +2 in the prologue, for block rb + 3 in step t (block rb) -- into the buffer that
+  //           held block rb - 1;
+  //   drained: by the qa fragment reads of step t only;
+  //   separated: the reads of block rb - 1 (step t - 1) from the fill in step t by the end of step
+  //           t - 1: lgkmcnt(0) (this wavefront's reads done) and s_barrier (every wavefront's);
+  //           the fill of block rb (step t - 3, or the prologue's vmcnt(0)) from its reads by the
+  //           vmcnt(4) of step t - 1 (of the 2 per step issued after it, only the last two steps'
+  //           may be outstanding) and the same barrier. The peeled last steps keep the count (loads
+  //           past the last block read zero rows into buffers nobody reads), and wait_loads() at
+  //           the end leaves no load in flight into LDS when the workgroup ends.
   __shared__ __attribute__((aligned(16))) uint16_t sQ0[TILE * D];
   __shared__ __attribute__((aligned(16))) uint16_t sQ1[TILE * D];
   __shared__ __attribute__((aligned(16))) uint16_t sQ2[TILE * D];
@@ -1212,6 +1224,27 @@ __global__ __launch_bounds__(NTHREADS, G == 1 ? 3 : 2) void fwd64_kernel(
   using frag = OP::frag;
   constexpr int D = 64, NS = 4, DB = 2, AS = 2;
   static_assert(G == 1 || G == 2, "one or two heads per wavefront");
+  // LDS lifetimes (tile t = key tile wg_end - 1 - t; every fill is a direct load of all four
+  // wavefronts, a quarter each, and each tile step ends with wait_loads() -- this wavefront's loads
+  // have landed -- and __syncthreads() -- every wavefront's have, and every wavefront is past its
+  // reads of the step):
+  //   sB0, sB1  tile t's K and V rows, buffer t mod 2. Filled: the prologue (tile 0), tile step
+  //             t - 1 (tile t). Drained: tile step t (the logit and value products). Separated:
+  //             the last reads of buffer t mod 2 (tile step t - 2) from its fill (tile step t - 1)
+  //             by the end of tile step t - 2.
+  //   sS0, sS1  tile t's head-0 K rows and each wavefront's carry row, buffer t mod 2. Filled: the
+  //             prologue (tiles 0, 1), tile step t - 2 (tile t). Drained: the selection of tile t
+  //             (select(), run at the end of tile step t - 1; tile 0's in the sweep's prologue).
+  //             Separated: the selection of tile t - 2 (end of tile step t - 3) from the fill in tile
+  //             step t - 2 by the end of tile step t - 3; tile 0's selection from tile 2's fill (tile
+  //             step 0) by the barrier after it in the sweep's prologue; the fill of tile t (tile
+  //             step t - 2) from its selection (end of tile step t - 1) by the end of tile step t - 2.
+  //   sF        per wavefront, its F tile: written by select() of tile t + 1 at the end of tile step t
+  //             (transposing stores), read at the start of tile step t + 1; the same wavefront's
+  //             writes follow its reads of tile t in program order, and the reads of tile t + 1 follow
+  //             the writes across the step's barrier.
+  //   sDamp     per wavefront, its queries' damping factors: written once before the prologue's
+  //             barrier, read only after it.
   __shared__ FwdTileBuf64<G> sB0, sB1;   // tile t's K and V rows in buffer t mod 2
   __shared__ FwdSelBuf64 sS0, sS1;    // tile t's head-0 K rows and carry rows in buffer t mod 2
   constexpr int LDF = TILE + 4;
@@ -2171,6 +2204,20 @@ __global__ __launch_bounds__(NTHREADS, 2) void bwd_kv64_kernel(
   // every access names its buffer at compile time: the compiler then knows the direct loads into
   // one buffer do not write what the tile reads from the other, and waits for them only at the end
   // of the tile (a single array indexed by tile parity made it wait before the tile's first read).
+  // LDS lifetimes (tile t = query tile NB - 1 - t):
+  //   sB0, sB1  tile t's Q, dO and head 0's Q rows, its rows' lse and -dbar, each wavefront's carry
+  //             row, buffer t mod 2. Filled: by direct loads of all four wavefronts (rows a quarter
+  //             each; statistics by wavefronts 0 and 1; each its own carry row), for tile 0 before
+  //             the first barrier, for tile t in tile step t - 1. Drained: tile step t only (every
+  //             product's fragment reads, rows16 / p_dz_tile of the statistics, the carry value; a
+  //             wavefront with no pair in the tile reads nothing but still loads and synchronises).
+  //             Separated: each tile step ends with wait_loads() (this wavefront's loads into the
+  //             other buffer have landed) and __syncthreads() (every wavefront's have, and every
+  //             wavefront is past its reads of this buffer), so the fill in tile step t + 1 of the
+  //             buffer tile step t read follows that barrier, and tile step t + 1's reads of the
+  //             buffer filled in tile step t follow it too. The last tile step loads nothing.
+  //   sV        per wavefront, its own V rows: written once with plain stores before the first
+  //             barrier, only read after it.
   __shared__ KvTileBuf64 sB0, sB1;
   __shared__ __attribute__((aligned(16))) elem sV[NWAVES][TW];
 
@@ -2310,14 +2357,22 @@ __global__ __launch_bounds__(NTHREADS, 2) void bwd_kv64_kernel(
         const bool split = !INTERIOR && split_keys;
         const TileMasks mk(j, qbase, T, exempt, h);
         auto body = [&]() {
+          // (keys past the end read a zero carry through the load's range check)
           const float hist = B.hist[wave][lane];
           const elem* q0s = H0 ? B.r[0] : B.r[2];
+          // the four fragments of head 0's Q rows are all requested before the chain of logit
+          // products starts, so the chain waits for one LDS latency rather than one per product
+          // (the default scheduler otherwise issues each read just before its product)
+          frag q0r[NS];
+#pragma unroll
+          for (int s = 0; s < NS; ++s) q0r[s] = rfrag(q0s, s);
+          __builtin_amdgcn_sched_barrier(0);
           f32x16 l0 = zero16();
 #pragma unroll
-          for (int s = 0; s < NS; ++s) l0 = OP::mma(rfrag(q0s, s), H0 ? kf[s] : k0f[s], l0);
+          for (int s = 0; s < NS; ++s) l0 = OP::mma(q0r[s], H0 ? kf[s] : k0f[s], l0);
           f32x16 fs;
           uint32_t gate;
-          selection_tile<false>(l0, (j < T) ? hist * neg_inv_scale : 0.f, h, edge, mk, gate, fs);
+          selection_tile<false>(l0, hist * neg_inv_scale, h, edge, mk, gate, fs);
 
           f32x16 lg;   // q.k - F/s
           if constexpr (H0) {   // head 0 itself: its logits are l0
@@ -2750,6 +2805,21 @@ __global__ __launch_bounds__(DQ64_WAVES * 64, 1) void bwd_dq64_kernel(
   using elem = uint16_t;
   using frag = OP::frag;
   constexpr int D = 64, NS = 4, DB = 2, AS = 2;
+  // LDS lifetimes (key tile t):
+  //   sB0, sB1  tile t's K, head 0's K and V rows, each wavefront's carry and U-checkpoint values,
+  //             buffer t mod 2. Filled: by direct loads (K rows by wavefronts 0-3, V rows by 4-7, a
+  //             quarter each; every wavefront its own carry and checkpoint values), tile 0 before the
+  //             first barrier, tile t in tile step t - 1. Drained: tile step t only (a wavefront
+  //             whose diagonal lies before tile t reads nothing but still loads and synchronises).
+  //             Separated: as in bwd_kv64_kernel, each tile step ends with wait_loads() and
+  //             __syncthreads(), between the last reads of a buffer and its next fill, and between a
+  //             fill and its reads. The last tile step loads nothing.
+  //   sZ        per wavefront, the dz / g tile transposed for the dQ products: written and read by
+  //             the same wavefront within a product (acc_xk); the LDS performs one wavefront's
+  //             operations in issue order, so lds_wave_order (a compiler barrier) keeps each read
+  //             after its write and the next write after the reads.
+  //   sRow      per wavefront, its rows' lse and -dbar: written once before the first barrier, only
+  //             read after it.
   __shared__ DqTileBuf64 sB0, sB1;
   __shared__ __attribute__((aligned(16))) elem sZ[DQ64_WAVES][TILE * TILE];   // per wavefront: dz, g transposed
   __shared__ __attribute__((aligned(16))) float sRow[DQ64_WAVES][2][TILE];   // per wavefront: its rows' lse, -dbar
