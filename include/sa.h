@@ -153,8 +153,10 @@ int64_t sa_backward_workspace_bytes(int64_t nseq, int64_t heads, int64_t t, int6
  * group: heads per wavefront of the backward kernels (0 = automatic); the workspace size depends
  * on it. Two kernels replace the reference's one: a key-parallel pass (dK, dV) and a
  * query-parallel pass (dQ), so no gradient element is accumulated with per-tile atomics.
- * The kernels write dq, dk, dv of every head but 0 directly; q, k, v, dout, dq, dk, dv 16-byte
- * aligned.
+ * The kernels write dq, dk, dv of every head but 0 directly; head 0's dq, dk are its own sums
+ * plus the other head groups' shares (one workspace slot per group), added in a fixed order by a
+ * finishing pass: no atomics anywhere, so repeated calls give the same bits. q, k, v, dout, dq,
+ * dk, dv 16-byte aligned.
  */
 int sa_backward(const void* q, const void* k, const void* v, const float* out, const void* dout,
                 const float* rmax, const float* rden, const float* carry,

@@ -105,8 +105,9 @@ __host__ __device__ inline int64_t utri_row(int64_t qb) { return (TILE / 2) * qb
 __host__ __device__ inline int64_t utri_floats(int64_t NB) { return utri_row(NB); }
 
 // Workspace of sa_backward: transposed Q, dO, K; row statistics; head 0's fp32 dQ, dK sums and
-// its shares from the other groups (every other gradient goes straight to the caller's views);
-// the selection-suffix checkpoints (one lower-triangular plane per head group and sequence).
+// its shares from the other groups, one slot per group (every other gradient goes straight to the
+// caller's views); the selection-suffix checkpoints (one lower-triangular plane per head group and
+// sequence).
 inline BwdLayout bwd_layout(int64_t nseq, int64_t heads, int64_t t, int64_t D, int64_t esize, int64_t G) {
   const int64_t R = nseq * heads, ldt = sa_transposed_ld(t), NB = (t + TILE - 1) / TILE;
   BwdLayout L;
@@ -122,8 +123,8 @@ inline BwdLayout bwd_layout(int64_t nseq, int64_t heads, int64_t t, int64_t D, i
   L.dbar = take(R * ldt * 4);   // -dbar, likewise
   L.dq = take(nseq * t * D * 4);   // head 0's own fp32 sums (the other heads write their views)
   L.dk = take(nseq * t * D * 4);
-  L.dq0x = take(nseq * t * D * 4);
-  L.dk0x = take(nseq * t * D * 4);
+  L.dq0x = take((heads / G - 1) * nseq * t * D * 4);   // groups 1 .. heads/G - 1: slots 0 ..
+  L.dk0x = take((heads / G - 1) * nseq * t * D * 4);
   L.ucheck = take((heads / G) * nseq * utri_floats(NB) * 4);
   L.total = off;
   return L;

@@ -25,8 +25,9 @@
 //                diagonal, recomputing P, dz and the selection gradient g from the key side's
 //                U checkpoints; dQ = dz K takes dz through a per-wavefront LDS tile.
 //   bwd_finish   gradient epilogue: scale, add head 0's shares, convert to the output dtype.
-// The group holding head 0 folds g = -gate*U into head 0's own dz; other groups add their share
-// of head 0's gradients with atomics.
+// The group holding head 0 folds g = -gate*U into head 0's own dz; every other group stores its
+// share of head 0's gradients in a slot of its own, and bwd_finish sums the slots in a fixed order
+// (no atomics: the backward is bitwise repeatable).
 //
 // MFMA operand layouts used throughout (v_mfma_f32_32x32x16_bf16 / v_mfma_f32_32x32x2_f32):
 //   C (32x32, 16 fp32 per lane): lane l holds column l%32, rows crow(i, l/32), i = 0..15,
@@ -1545,16 +1546,10 @@ template <class OP, int D>
 __global__ __launch_bounds__(NTHREADS) void bwd_rowstats_kernel(
     const typename OP::elem* __restrict__ dout, Strides dos, int H, int T, const float* __restrict__ out,
     const float* __restrict__ rmax, const float* __restrict__ rden,
-    float* __restrict__ lse, float* __restrict__ ndbar, int64_t ldt, int64_t rows, float4* __restrict__ zero0,
-    float4* __restrict__ zero1, int64_t zero_n4) {
+    float* __restrict__ lse, float* __restrict__ ndbar, int64_t ldt, int64_t rows) {
   using elem = typename OP::elem;
   constexpr int LPR = D / 8;   // lanes per row
   const int64_t g = (int64_t)blockIdx.x * NTHREADS + threadIdx.x;
-  // also clears the targets of the head-0 share atomics (zero_n4 float4s each)
-  for (int64_t i = g; i < zero_n4; i += (int64_t)gridDim.x * NTHREADS) {
-    zero0[i] = make_float4(0.f, 0.f, 0.f, 0.f);
-    zero1[i] = make_float4(0.f, 0.f, 0.f, 0.f);
-  }
   const int64_t pr = g / LPR;   // padded row: head pr / ldt, row t
   const int part = (int)(g % LPR);
   const int64_t hr = pr / ldt;   // b * H + head
@@ -2159,12 +2154,15 @@ __global__ __launch_bounds__(NTHREADS, (kv_min_blocks<OP, D, G>())) void bwd_kv_
         else store_grad4(dkv, b, hh, j, d, kq);
       }
   }
-  if (!has_h0) {
-    float* dst = dk0x + ((int64_t)b * T + j) * D;
+  if (!has_h0) {   // this group's share of head 0's dK, in its own slot (group gi: slot gi - 1)
+    float* dst = dk0x + ((int64_t)(gi - 1) * nseq * T + (int64_t)b * T + j) * D;
 #pragma unroll
     for (int db = 0; db < DB; ++db)
 #pragma unroll
-      for (int i = 0; i < 16; ++i) atomicAdd(dst + db * 32 + crow(i, h), dk0t[db][i] * scale);
+      for (int a = 0; a < 4; ++a)
+        *reinterpret_cast<float4*>(dst + db * 32 + 8 * a + 4 * h) =
+            make_float4(dk0t[db][4 * a] * scale, dk0t[db][4 * a + 1] * scale, dk0t[db][4 * a + 2] * scale,
+                        dk0t[db][4 * a + 3] * scale);
   }
 }
 
@@ -2439,12 +2437,15 @@ __global__ __launch_bounds__(NTHREADS, 2) void bwd_kv64_kernel(
       if (has_h0 && H > 1) *reinterpret_cast<float4*>(dk0h + ((int64_t)b * T + j) * D + d) = kq;
       else store_grad4(dkv, b, hh, j, d, kq);
     }
-  if (!has_h0) {
-    float* dst = dk0x + ((int64_t)b * T + j) * D;
+  if (!has_h0) {   // this head's share of head 0's dK, in its own slot (head hh: slot hh - 1)
+    float* dst = dk0x + ((int64_t)(hh - 1) * nseq * T + (int64_t)b * T + j) * D;
 #pragma unroll
     for (int db = 0; db < DB; ++db)
 #pragma unroll
-      for (int i = 0; i < 16; ++i) atomicAdd(dst + db * 32 + crow(i, h), dk0t[db][i] * scale);
+      for (int a = 0; a < 4; ++a)
+        *reinterpret_cast<float4*>(dst + db * 32 + 8 * a + 4 * h) =
+            make_float4(dk0t[db][4 * a] * scale, dk0t[db][4 * a + 1] * scale, dk0t[db][4 * a + 2] * scale,
+                        dk0t[db][4 * a + 3] * scale);
   }
 }
 
@@ -2761,13 +2762,14 @@ __global__ __launch_bounds__(NTHREADS, (dq_min_blocks<OP, D>())) void bwd_dq_ker
       }
     }
   }
-  if (!has_h0) {
+  if (!has_h0) {   // this group's share of head 0's dQ (unscaled), in its own slot (group gi: slot gi - 1)
+    float* dst = dq0x + ((int64_t)(gi - 1) * nseq * T + (int64_t)b * T) * D;
 #pragma unroll
     for (int i = 0; i < 16; ++i) {
       const int r = qbase + crow(i, h);
       if (r < T) {
 #pragma unroll
-        for (int db = 0; db < DB; ++db) atomicAdd(dq0x + ((int64_t)b * T + r) * D + db * 32 + n, dq0acc[db][i]);
+        for (int db = 0; db < DB; ++db) dst[(int64_t)r * D + db * 32 + n] = dq0acc[db][i];
       }
     }
   }
@@ -3028,30 +3030,37 @@ __global__ __launch_bounds__(DQ64_WAVES * 64, 1) void bwd_dq64_kernel(
       }
     }
   }
-  if (!has_h0) {
+  if (!has_h0) {   // this head's share of head 0's dQ (unscaled), in its own slot (head hh: slot hh - 1)
+    float* dst = dq0x + ((int64_t)(hh - 1) * nseq * T + (int64_t)b * T) * D;
 #pragma unroll
     for (int i = 0; i < 16; ++i) {
       const int r = qbase + crow(i, h);
       if (r < T) {
 #pragma unroll
-        for (int db = 0; db < DB; ++db) atomicAdd(dq0x + ((int64_t)b * T + r) * D + db * 32 + n, dq0acc[db][i]);
+        for (int db = 0; db < DB; ++db) dst[(int64_t)r * D + db * 32 + n] = dq0acc[db][i];
       }
     }
   }
 }
 
-// Head 0's gradients: its own fp32 sums plus the other groups' shares, (b, t, D) contiguous, four
-// elements per thread, to the caller's views.
+// Head 0's gradients: its own fp32 sums plus the other groups' shares, summed slot after slot in
+// group order (so every run adds the same values in the same order), (b, t, D) contiguous, four
+// elements per thread, to the caller's views. nslots slots of total4 float4s each.
 __global__ __launch_bounds__(NTHREADS) void bwd_finish_kernel(
     const float4* __restrict__ dq0h, const float4* __restrict__ dk0h, const float4* __restrict__ dq0x,
-    const float4* __restrict__ dk0x, GradView dqv, GradView dkv, int D, int64_t TD, int64_t total4, float scale) {
+    const float4* __restrict__ dk0x, int nslots, GradView dqv, GradView dkv, int D, int64_t TD, int64_t total4,
+    float scale) {
   for (int64_t e = (int64_t)blockIdx.x * NTHREADS + threadIdx.x; e < total4; e += (int64_t)gridDim.x * NTHREADS) {
     const int64_t b = (4 * e) / TD, off = 4 * e - b * TD;
     const int t = (int)(off / D), d = (int)(off - (int64_t)t * D);
-    const float4 q = dq0h[e], qx = dq0x[e], k = dk0h[e], kx = dk0x[e];
-    store_grad4(dqv, b, 0, t, d, make_float4((q.x + qx.x) * scale, (q.y + qx.y) * scale, (q.z + qx.z) * scale,
-                                             (q.w + qx.w) * scale));
-    store_grad4(dkv, b, 0, t, d, make_float4(k.x + kx.x, k.y + kx.y, k.z + kx.z, k.w + kx.w));
+    float4 q = dq0h[e], k = dk0h[e];
+    for (int sl = 0; sl < nslots; ++sl) {
+      const float4 qx = dq0x[sl * total4 + e], kx = dk0x[sl * total4 + e];
+      q = make_float4(q.x + qx.x, q.y + qx.y, q.z + qx.z, q.w + qx.w);
+      k = make_float4(k.x + kx.x, k.y + kx.y, k.z + kx.z, k.w + kx.w);
+    }
+    store_grad4(dqv, b, 0, t, d, make_float4(q.x * scale, q.y * scale, q.z * scale, q.w * scale));
+    store_grad4(dkv, b, 0, t, d, k);
   }
 }
 
@@ -3552,11 +3561,7 @@ int backward_impl(const BwdCall& c) {
     launch_transpose<elem, D>(k, kt, T, ldt, c.ks, H, R, st);
   }
   hipLaunchKernelGGL((bwd_rowstats_kernel<OP, D>), dim3((unsigned)cdiv(R * ldt * (D / 8), NTHREADS)),
-                     dim3(NTHREADS), 0, st, dout, c.dos, H, T, c.out, c.rmax, c.rden, lse, dbar, ldt, R * ldt,
-                     // head 0's shares from the other groups are atomic targets (one add per element
-                     // and group): cleared here (a one-head sequence has none)
-                     reinterpret_cast<float4*>(dq0x), reinterpret_cast<float4*>(dk0x),
-                     H > 1 ? (int64_t)nseq * T * D / 4 : 0);
+                     dim3(NTHREADS), 0, st, dout, c.dos, H, T, c.out, c.rmax, c.rden, lse, dbar, ldt, R * ldt);
   int rc = launch_status();   // the transposes and row statistics
   if (rc) return rc;
 #define SA_LAUNCH_BWD(GG) launch_bwd<OP, D, GG>(c, qt, kt, dot, lse, dbar, ucheck, dq0h, dk0h, dq0x, dk0x, ldt)
@@ -3574,7 +3579,8 @@ int backward_impl(const BwdCall& c) {
   hipLaunchKernelGGL(bwd_finish_kernel, dim3((unsigned)std::min<int64_t>(cdiv(total4, NTHREADS), 8192)),
                      dim3(NTHREADS), 0, st, reinterpret_cast<const float4*>(dq0h),
                      reinterpret_cast<const float4*>(dk0h), reinterpret_cast<const float4*>(dq0x),
-                     reinterpret_cast<const float4*>(dk0x), GradView{c.dq, c.dqs, f32}, GradView{c.dk, c.dks, f32}, D,
+                     reinterpret_cast<const float4*>(dk0x), H / G - 1, GradView{c.dq, c.dqs, f32},
+                     GradView{c.dk, c.dks, f32}, D,
                      (int64_t)T * D, total4, c.scale);
   return launch_status();
 }

@@ -53,10 +53,11 @@ def test_workspace_sizes():
     assert lib.sa_forward_workspace_bytes(1, 16, 16384, 64, 1, 0) >= 16 * 64 * 16384 * 4
     bw = lib.sa_backward_workspace_bytes(1, 16, 16384, 64, 0, 0)
     # the 16 head groups' U checkpoints (the causal part of each 512 x 16384 plane: 32 x 512 x 513 / 2
-    # floats), head 0's fp32 dq and dk (and the other groups' shares), lse and -dbar; no transposed
-    # copies (at bf16 head dim 64 the kernels read Q, dO and K transposed from LDS)
+    # floats), head 0's fp32 dq and dk and the other 15 groups' shares of them (one slot each, so the
+    # finishing sum runs in a fixed order), lse and -dbar; no transposed copies (at bf16 head dim 64
+    # the kernels read Q, dO and K transposed from LDS)
     tri = 16 * 512 * 513
-    fixed = 16 * tri * 4 + 4 * 16384 * 64 * 4 + 2 * 16 * 16384 * 4
+    fixed = 16 * tri * 4 + (2 + 2 * 15) * 16384 * 64 * 4 + 2 * 16 * 16384 * 4
     assert bw >= fixed and bw % 256 == 0
     assert bw < fixed + 4096
     # other head dims (and fp32 storage) keep the Q^T, dO^T and K^T copies
