@@ -334,10 +334,10 @@ __device__ __forceinline__ void stage_cols(E* s, const E* g, int64_t gld, int co
   }
 }
 
-// The dispatcher deals workgroups round-robin to the 8 XCDs, each with its own L2. The attention
-// kernels remap the linear workgroup id so that every XCD takes a contiguous range of the
+// The dispatcher deals workgroups round-robin to the 8 XCDs, each with its own L2. The forward and
+// selection kernels remap the linear workgroup id so that every XCD takes a contiguous range of the
 // (head group, block) order instead: the workgroups one L2 serves at a time then belong to one or
-// two heads and share that head's tiles.
+// two heads and share that head's tiles (the backward kernels' order is work_order_block, below).
 constexpr int NXCD = 8;
 struct BlockXY {
   int x, y;
@@ -348,6 +348,18 @@ __device__ __forceinline__ BlockXY xcd_block() {
   const int per = n / NXCD;
   const int m = (l < per * NXCD) ? (l % NXCD) * per + l / NXCD : l;
   return {m % gx, m / gx};
+}
+
+// The backward kernels' order: x-major (x the block, whose work falls as x grows; y the head row),
+// so the round-robin deal gives every XCD every eighth workgroup of a list sorted by work: each XCD
+// runs its share longest first and the XCDs' shares stay even whatever the head count. (With the
+// contiguous ranges of xcd_block, 12 heads leave one XCD a third more work than the mean: the
+// backward at the reference's 12-head geometry ran as long as at 16 heads.) An XCD still serves
+// few heads at a time -- heads i and i + 8 at a multiple of 8 -- whose tiles it shares in its L2.
+__device__ __forceinline__ BlockXY work_order_block() {
+  const int gy = gridDim.y;
+  const int l = blockIdx.x + gridDim.x * blockIdx.y;
+  return {l / gy, l % gy};
 }
 
 // Unpadded LDS rows of 64 bf16 (eight 16-byte chunks), chunk c of row r stored at chunk position
@@ -1870,7 +1882,7 @@ __global__ __launch_bounds__(NTHREADS, (kv_min_blocks<OP, D, G>())) void bwd_kv_
   const int tid = threadIdx.x, lane = tid & 63, wave = wave_id();
   const int n = lane & 31, h = lane >> 5;
   const int groups = H / G;
-  const BlockXY bxy = xcd_block();
+  const BlockXY bxy = work_order_block();
   const int b = bxy.y / groups, gi = bxy.y % groups;
   const int hd0 = gi * G;
   const bool has_h0 = (gi == 0);
@@ -2221,7 +2233,7 @@ __global__ __launch_bounds__(NTHREADS, 2) void bwd_kv64_kernel(
 
   const int tid = threadIdx.x, lane = tid & 63, wave = wave_id();
   const int n = lane & 31, h = lane >> 5;
-  const BlockXY bxy = xcd_block();
+  const BlockXY bxy = work_order_block();
   const int b = bxy.y / H, hh = bxy.y % H;
   const bool has_h0 = (hh == 0);
   const int NB = (T + TILE - 1) / TILE;
@@ -2483,7 +2495,7 @@ __global__ __launch_bounds__(NTHREADS, (dq_min_blocks<OP, D>())) void bwd_dq_ker
   const int tid = threadIdx.x, lane = tid & 63, wave = wave_id();
   const int n = lane & 31, h = lane >> 5;
   const int groups = H / G;
-  const BlockXY bxy = xcd_block();
+  const BlockXY bxy = work_order_block();
   const int b = bxy.y / groups, gi = bxy.y % groups;
   const int hd0 = gi * G;
   const bool has_h0 = (gi == 0);
@@ -2828,7 +2840,7 @@ __global__ __launch_bounds__(DQ64_WAVES * 64, 1) void bwd_dq64_kernel(
 
   const int tid = threadIdx.x, lane = tid & 63, wave = wave_id();
   const int n = lane & 31, h = lane >> 5;
-  const BlockXY bxy = xcd_block();
+  const BlockXY bxy = work_order_block();
   const int b = bxy.y / H, hh = bxy.y % H;
   const bool has_h0 = (hh == 0);
   const int NB = (T + TILE - 1) / TILE;
