@@ -96,7 +96,8 @@ int64_t sa_forward_workspace_bytes(int64_t nseq, int64_t heads, int64_t tk, int6
  * layout); a prefill over a preallocated (nseq, heads, capacity, head_dim) cache passes
  * capacity * head_dim, so no prefix is copied. A multiple of 8.
  * scale: the logit scale s (the reference uses 1/sqrt(D); a caller that zero-pads D passes the
- * unpadded value). group: heads per wavefront (0 = automatic); damp_mode 0 none, 1 linear, 2 sqrt scales F of
+ * unpadded value). group: heads per wavefront (0 = automatic: at bf16 head dim 64 two, or one when
+ * the two-head grid would fill the CUs only once; both give the same bits there); damp_mode 0 none, 1 linear, 2 sqrt scales F of
  * query i by min(1, train_len/(i+1)) (or its square root), reference kernels.py:179-182.
  * Limits (all entry points): one head's rows below 2 GiB ((t + 64) * row stride * element size
  * < 2^31; the row stride is head_dim here).

@@ -8,6 +8,7 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <algorithm>
 #include <mutex>
 #include <utility>
 #include <vector>
@@ -82,6 +83,33 @@ inline int auto_group(int dtype, int64_t D, int64_t heads, int requested, bool b
   g = g > cap ? cap : g;
   while (g > 1 && (heads % g != 0)) g >>= 1;
   return g < 1 ? 1 : g;
+}
+
+// Heads per wavefront of the bf16 head-dim-64 forward when the caller leaves the choice open and
+// auto_group allows two. Two heads per wavefront share head 0's selection and run two workgroups per
+// CU; one head per wavefront runs three per CU with half the work per workgroup, and gives the same
+// bits (fwd64_kernel). Two win once their grid needs more than one round of workgroups (more than two
+// per CU): the dispatch order (part_block) then balances the XCDs and the cheaper head-tiles tell.
+// With one round or less the launch lasts about as long as its longest workgroup -- the last query
+// rows' sweep over every key -- which one head per wavefront halves. Measured on MI355X (forward call,
+// ms, one / two heads per wavefront, B x H x T): 1x16x16384 1.27 / 0.99, 1x12x16384 0.90 / 0.71,
+// 2x12x8192 0.46 / 0.36, 4x16x4096 0.33 / 0.27 (more than one round); 1x8x16384 0.61 / 0.65,
+// 1x16x8192 0.31 / 0.33, 1x12x8192 0.28 / 0.32, 2x12x4096 0.15 / 0.17, 1x2x16384 0.50 / 0.62 (one
+// round or less).
+inline int fwd64_group(int64_t nseq, int64_t heads, int64_t tq, int cus) {
+  if (heads % 2 != 0) return 1;
+  const int64_t workgroups = nseq * (heads / 2) * cdiv(cdiv(tq, TILE), NWAVES);
+  return workgroups > 2 * (int64_t)cus ? 2 : 1;
+}
+
+// Compute units of the current device (256 on MI355X, the figure used when the query fails).
+inline int device_cus() {
+  int dev = 0, n = 0;
+  if (hipGetDevice(&dev) != hipSuccess || hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) {
+    (void)hipGetLastError();   // (the launches' status check reads the last error)
+    return 256;
+  }
+  return n > 0 ? n : 256;
 }
 
 // Heads per wavefront of the backward kernels: a group shares head 0's selection work (its logits,

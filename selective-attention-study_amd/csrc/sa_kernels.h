@@ -334,10 +334,11 @@ __device__ __forceinline__ void stage_cols(E* s, const E* g, int64_t gld, int co
   }
 }
 
-// The dispatcher deals workgroups round-robin to the 8 XCDs, each with its own L2. The forward and
-// selection kernels remap the linear workgroup id so that every XCD takes a contiguous range of the
-// (head group, block) order instead: the workgroups one L2 serves at a time then belong to one or
-// two heads and share that head's tiles (the backward kernels' order is work_order_block, below).
+// The dispatcher deals workgroups round-robin to the 8 XCDs, each with its own L2. The selection
+// kernels and the generic forward remap the linear workgroup id so that every XCD takes a contiguous
+// range of the (head group, block) order instead: the workgroups one L2 serves at a time then belong
+// to one or two heads and share that head's tiles (the direct-load forward's order is part_block, the
+// backward kernels' work_order_block, below).
 constexpr int NXCD = 8;
 struct BlockXY {
   int x, y;
@@ -360,6 +361,26 @@ __device__ __forceinline__ BlockXY work_order_block() {
   const int gy = gridDim.y;
   const int l = blockIdx.x + gridDim.x * blockIdx.y;
   return {l / gy, l % gy};
+}
+
+// The direct-load forward's order: every XCD takes an equal share of the work from as few head
+// groups as that allows, longest first. Each row y (one head group of one sequence, its blocks x
+// ordered longest first) is cut into P parts by x mod P, P = 8 / gcd(gy, 8), so that the gy * P
+// parts divide evenly over the 8 XCDs; the parts of a row hold nearly equal work. XCD i takes parts
+// [i m, i m + m), m = gy P / 8 (one row's worth or a little more), and runs them x-major: block by
+// block, longest first. With gy a multiple of 8 and one row per XCD this is xcd_block's order; with
+// 6 or 12 rows (the 12 heads of the reference's model, in pairs) xcd_block's contiguous ranges give
+// one XCD the long blocks of a row and another its short ones (measured: a third more work on the
+// busiest XCD). A grid whose x extent P does not divide falls back to xcd_block.
+__device__ __forceinline__ BlockXY part_block() {
+  const int gx = gridDim.x, gy = gridDim.y;
+  const int P = NXCD >> min(__builtin_ctz((unsigned)gy), 3);   // 8 / gcd(gy, 8)
+  if (gx % P != 0) return xcd_block();
+  const int m = gy * P / NXCD;
+  const int l = blockIdx.x + gx * blockIdx.y;
+  const int r = l / NXCD;
+  const int part = (l % NXCD) * m + r % m;
+  return {part % P + (r / m) * P, part / P};
 }
 
 // Unpadded LDS rows of 64 bf16 (eight 16-byte chunks), chunk c of row r stored at chunk position
@@ -1202,19 +1223,20 @@ __global__ __launch_bounds__(NTHREADS, (fwd_min_blocks<OP, D, G>())) void fwd_ke
 }
 
 // ---------------------------------------------------------------------------------------------
-// Forward, bf16 storage at head dim 64 with G = 2 heads per wavefront (the default there) or one
-// (odd head counts, the per-head mode): fwd_kernel's tile work with every key tile's operands loaded
-// straight into LDS ahead of use (see bwd_kv64_kernel), and the selection one tile ahead of the
-// softmax: while tile t's logit products, softmax and value products run, the wavefront also takes
-// head 0's logits of tile t + 1 and turns them into that tile's F (through its LDS rows, read at the
-// start of tile t + 1), so each tile is one block of independent products and arithmetic the
-// compiler interleaves, with no wait inside it for the F round trip. A one-head group holding head 0
-// sends that head's whole adjusted logits through the LDS rows instead (as fwd_kernel does), so it
-// takes one logit product per tile. The K rows of the group's heads (swz64) and their V rows (swzq,
-// read transposed by the value products, get_trq) load one tile ahead into two buffers; head 0's K rows and each wavefront's carry row two tiles
-// ahead into two more; all four are separate LDS variables and the tile loop runs in pairs, so every
-// access names its buffer at compile time; one barrier per tile. Two workgroups per CU at G = 2,
-// three at G = 1.
+// Forward, bf16 storage at head dim 64 with G = 2 heads per wavefront or one (odd head counts, the
+// per-head mode, grids that fill the CUs only once: fwd64_group): fwd_kernel's tile work with every
+// key tile's operands loaded straight into LDS ahead of use (see bwd_kv64_kernel), and the
+// selection one tile ahead of the softmax: while tile t's logit products, softmax and value
+// products run, the wavefront also takes head 0's logits of tile t + 1 and turns them into that
+// tile's F (through its LDS rows, read at the start of tile t + 1), so each tile is one block of
+// independent products and arithmetic the compiler interleaves, with no wait inside it for the F
+// round trip. A sequence's only head (G = 1, one head) sends its whole adjusted logits through the
+// LDS rows instead (as fwd_kernel does), so it takes one logit product per tile. The K rows of the
+// group's heads (swz64) and their V rows (swzq, read transposed by the value products, get_trq)
+// load one tile ahead into two buffers; head 0's K rows and each wavefront's carry row two tiles
+// ahead into two more; all four are separate LDS variables and the tile loop runs in pairs, so
+// every access names its buffer at compile time; one barrier per tile. Two workgroups per CU at
+// G = 2, three at G = 1.
 
 template <int G>
 struct FwdTileBuf64 {
@@ -1267,11 +1289,15 @@ __global__ __launch_bounds__(NTHREADS, G == 1 ? 3 : 2) void fwd64_kernel(
   const int tid = threadIdx.x, lane = tid & 63, wave = wave_id();
   const int n = lane & 31, h = lane >> 5;
   const int groups = H / G;
-  const BlockXY bxy = xcd_block();
+  const BlockXY bxy = part_block();
   const int b = bxy.y / groups, gi = bxy.y % groups;
   const int hd0 = gi * G;
   const bool has_h0 = (gi == 0);
-  const bool whole = G == 1 && has_h0;   // head 0's adjusted logits come through LDS whole
+  // Head 0's adjusted logits come through LDS whole when it is the sequence's only head (one product
+  // per tile instead of two). With other heads beside it, head 0 takes the path of every head (its
+  // product accumulating onto -F), so one and two heads per wavefront give the same bits and the
+  // host may choose either per launch.
+  const bool whole = G == 1 && has_h0 && H == 1;
   const int NBq = (Tq + TILE - 1) / TILE;
   const int NKT = (Tk + TILE - 1) / TILE;
   const int qsb = gridDim.x - 1 - bxy.x;
@@ -3438,7 +3464,10 @@ int forward_impl(const FwdCall& c) {
   const int64_t ldv = sa_transposed_ld(c.Tk);
   elem* vt = static_cast<elem*>(c.ws);
   const int dtype = sizeof(elem) == 2 ? SA_DTYPE_BF16 : SA_DTYPE_F32;
-  const int G = auto_group(dtype, D, c.H, c.group, false);
+  int G = auto_group(dtype, D, c.H, c.group, false);
+  if constexpr (sizeof(elem) == 2 && D == 64) {
+    if (c.group <= 0 && G == 2) G = fwd64_group(c.nseq, c.H, c.Tq, device_cus());
+  }
   // V^T for fwd_kernel (fwd64_kernel, bf16 at head dim 64 with G <= 2, reads the V rows transposed
   // from LDS)
   if (!(sizeof(elem) == 2 && D == 64 && G <= 2))

@@ -4,8 +4,10 @@ bf16-valued inputs (reference tests/test_selective_kernels.py:141-172, 203-242).
 The launch policy picks the instance from (head_dim, heads, group, bwd_group); with H = 4:
 
     forward   head_dim 16 / 32 (run at 32): group 1 -> 1 head per wavefront, 2 -> 2, 4 / None -> 4
-              head_dim 64:                  group 1 -> 1, 2 / None -> 2, 4 -> 4 (an odd head count
-                                            runs 1: the prefill cases at H = 3 and H = 1)
+              head_dim 64:                  group 1 -> 1, 2 -> 2, 4 -> 4, None -> 2, or 1 when
+                                            the two-head grid fills the CUs only once (the same bits:
+                                            test_fwd64_one_or_two_heads_per_wavefront_same_bits; an
+                                            odd head count runs 1: the prefill cases at H = 3 and 1)
               head_dim 128:                 1
     backward  head_dim 16 / 32: bwd_group 2 -> 2 heads per wavefront (key side and query side),
               1 / None -> 1;  head_dim 64, 128: 1
@@ -170,3 +172,28 @@ def test_bf16_head_dim_64_forward_short_sequences(cuda, seq, heads):
     total = sa_oracle.selection_totals(q.double(), k.double())
     err = (aux["selected_total"].cpu().double() - total).abs().max().item()
     assert err <= 1e-4 * max(total.abs().max().item(), 1.0), err
+
+
+@pytest.mark.parametrize("batch,heads,seq,exempt,damp", [(1, 4, 300, 1, None), (2, 12, 2047, 1, None),
+                                                         (1, 2, 4096, 16, None), (1, 16, 1024, 3, None),
+                                                         (1, 6, 700, 1, "linear")])
+def test_fwd64_one_or_two_heads_per_wavefront_same_bits(cuda, batch, heads, seq, exempt, damp):
+    """At head dim 64 the library chooses one or two heads per wavefront per launch (group=None) from
+    the size of the launch's grid; a shape's output must not depend on that choice, so that a prefix
+    of a longer run (which may launch with the other width) stays equal bit for bit. Both widths, and
+    the automatic choice, give the same output and selection state."""
+    print(f"case fwd64 widths B={batch} H={heads} T={seq} E={exempt} damp={damp}", flush=True)
+    q, k, v, _ = _inputs(batch, heads, seq, 64, seed=seq + heads, scale=1.2)
+    qd, kd, vd = (t.to(cuda) for t in (q, k, v))
+    kw = dict(exempt=exempt, return_aux=True)
+    if damp:
+        kw.update(damp=damp, train_len=seq // 3)
+    runs = [kernels.selective_attention_forward(qd, kd, vd, group=g, **kw) for g in (1, 2, None)]
+    for out, aux in runs[1:]:
+        assert torch.equal(out, runs[0][0])
+        assert torch.equal(aux["carry"], runs[0][1]["carry"])
+        assert torch.equal(aux["selected_total"], runs[0][1]["selected_total"])
+    if seq <= 1024 and not damp:   # and it is the oracle's
+        with torch.no_grad():
+            want = sa_oracle.attention(q.double(), k.double(), v.double(), exempt)
+        assert (runs[0][0].cpu().double() - want).abs().max().item() < 3e-2
