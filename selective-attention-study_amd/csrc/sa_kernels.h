@@ -368,14 +368,16 @@ __device__ __forceinline__ BlockXY work_order_block() {
 // ordered longest first) is cut into P parts by x mod P, P = 8 / gcd(gy, 8), so that the gy * P
 // parts divide evenly over the 8 XCDs; the parts of a row hold nearly equal work. XCD i takes parts
 // [i m, i m + m), m = gy P / 8 (one row's worth or a little more), and runs them x-major: block by
-// block, longest first. With gy a multiple of 8 and one row per XCD this is xcd_block's order; with
-// 6 or 12 rows (the 12 heads of the reference's model, in pairs) xcd_block's contiguous ranges give
-// one XCD the long blocks of a row and another its short ones (measured: a third more work on the
-// busiest XCD). A grid whose x extent P does not divide falls back to xcd_block.
+// block, longest first. With 6 or 12 rows (the 12 heads of the reference's model, in pairs)
+// xcd_block's contiguous ranges give one XCD the long blocks of a row and another its short ones
+// (measured: a third more work on the busiest XCD). With gy a multiple of 8 (P = 1) every XCD takes
+// whole rows and xcd_block's order, one row after another, is kept: interleaving an XCD's rows
+// doubled the forward's HBM fetches at 32 rows (C5's). A grid whose x extent P does not divide falls
+// back to xcd_block too.
 __device__ __forceinline__ BlockXY part_block() {
   const int gx = gridDim.x, gy = gridDim.y;
   const int P = NXCD >> min(__builtin_ctz((unsigned)gy), 3);   // 8 / gcd(gy, 8)
-  if (gx % P != 0) return xcd_block();
+  if (P == 1 || gx % P != 0) return xcd_block();
   const int m = gy * P / NXCD;
   const int l = blockIdx.x + gx * blockIdx.y;
   const int r = l / NXCD;
