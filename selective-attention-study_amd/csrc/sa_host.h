@@ -102,6 +102,20 @@ inline int fwd64_group(int64_t nseq, int64_t heads, int64_t tq, int cus) {
   return workgroups > 2 * (int64_t)cus ? 2 : 1;
 }
 
+// The dispatch order of the query-side backward kernel at head dim 64 (work_order_block): the number
+// of its workgroups an XCD runs at once when a launch holds 2.7 to 3 of them per slot, where the
+// order that follows each XCD's first round with its shortest workgroups balances the slots better
+// (a list-scheduling simulation: 1.03x the balanced share against 1.11x at 3.0; measured at the 12
+// heads of d768: 1.28 -> 1.18 ms); else 0, the longest-first order, which is already balanced at
+// whole even numbers of rounds and better everywhere else that was simulated (head counts 2-40 at
+// 8192 and 16384 tokens).
+inline int bwd_snake_slots(int64_t workgroups, int per_cu, int cus) {
+  const int64_t slots = (int64_t)(cus / 8) * per_cu;
+  if (slots <= 0) return 0;
+  const double rounds = (double)workgroups / (8.0 * (double)slots);
+  return (rounds >= 2.7 && rounds <= 3.0) ? (int)slots : 0;
+}
+
 // Compute units of the current device (256 on MI355X, the figure used when the query fails).
 inline int device_cus() {
   int dev = 0, n = 0;

@@ -363,6 +363,34 @@ __device__ __forceinline__ BlockXY work_order_block() {
   return {l / gy, l % gy};
 }
 
+// work_order_block with each XCD's share (every eighth workgroup of the longest-first list, n of
+// them) dispatched in a different order when `slots` (the workgroups an XCD runs at once) is
+// nonzero: its `slots` longest first, as before, then the shortest third of the rest, shortest
+// first, then the middle third, longest first. The dispatcher hands an XCD's next workgroup to
+// whichever slot frees first, so with about three workgroups per slot (the 12 heads of the
+// reference's model at 16384 tokens) a slot that ran a short first workgroup collects a run of the
+// shortest ones before the middle third arrives, and the slots end closer together than with the
+// longest-first order, whose third round leaves the spread of the middle third (a list-scheduling
+// simulation: 1.03x the balanced share against 1.11x). The query-side kernel takes it (one
+// workgroup per CU; the host passes `slots` only in that regime, bwd_snake_slots): at d768 1.28 ->
+// 1.18 ms per layer. The key side, two workgroups per CU, keeps the longest-first order: a
+// workgroup left alone on its CU speeds up once its CU-mate finishes, which already evens its
+// slots (1.20 ms there, three quarters of its 16-head time), and the other order ran it 3% slower.
+__device__ __forceinline__ BlockXY work_order_block(int slots) {
+  if (slots <= 0) return work_order_block();
+  const int gy = gridDim.y, total = gridDim.x * gy;
+  const int l = blockIdx.x + gridDim.x * blockIdx.y;
+  const int x8 = l % NXCD, p = l / NXCD;             // this XCD's p-th dispatch
+  const int n = (total - x8 + NXCD - 1) / NXCD;      // workgroups of this XCD
+  int q = p;                                         // rank in the XCD's longest-first list
+  if (p >= slots && n > slots) {
+    const int rest = n - slots, n_low = rest - rest / 2, pp = p - slots;
+    q = (pp < n_low) ? n - 1 - pp : slots + (pp - n_low);
+  }
+  const int g = q * NXCD + x8;
+  return {g / gy, g % gy};
+}
+
 // The direct-load forward's order: every XCD takes an equal share of the work from as few head
 // groups as that allows, longest first. Each row y (one head group of one sequence, its blocks x
 // ordered longest first) is cut into P parts by x mod P, P = 8 / gcd(gy, 8), so that the gy * P
@@ -2835,14 +2863,16 @@ struct DqTileBuf64 {
 };
 
 // CV: every view is the contiguous (nseq, H, T, D) layout of sa_backward. SOLO: one-head sequences
-// only (head 0's loop alone is built, as in bwd_kv64_kernel).
-template <bool CV, bool SOLO>
+// only (head 0's loop alone is built, as in bwd_kv64_kernel). SNAKE: workgroups dealt in the order
+// of work_order_block(order_slots) (an instance of its own, so the launches in the longest-first
+// order run exactly the code they ran before it existed; order_slots is unused there).
+template <bool CV, bool SOLO, bool SNAKE = false>
 __global__ __launch_bounds__(DQ64_WAVES * 64, 1) void bwd_dq64_kernel(
     const uint16_t* __restrict__ q, const uint16_t* __restrict__ k, const uint16_t* __restrict__ v,
     const uint16_t* __restrict__ dout, Strides qs, Strides ks, Strides vs, Strides dos,
     const float* __restrict__ lse, const float* __restrict__ dbar, const float* __restrict__ carry,
     const float* __restrict__ ucheck, float* __restrict__ dq0h, float* __restrict__ dq0x, GradView dqv, int nseq,
-    int H, int T, int64_t ldt, int exempt, float scale) {
+    int H, int T, int64_t ldt, int exempt, float scale, int order_slots) {
   using OP = OpBF16;
   using elem = uint16_t;
   using frag = OP::frag;
@@ -2868,7 +2898,7 @@ __global__ __launch_bounds__(DQ64_WAVES * 64, 1) void bwd_dq64_kernel(
 
   const int tid = threadIdx.x, lane = tid & 63, wave = wave_id();
   const int n = lane & 31, h = lane >> 5;
-  const BlockXY bxy = work_order_block();
+  const BlockXY bxy = SNAKE ? work_order_block(order_slots) : work_order_block();
   const int b = bxy.y / H, hh = bxy.y % H;
   const bool has_h0 = (hh == 0);
   const int NB = (T + TILE - 1) / TILE;
@@ -3551,16 +3581,20 @@ int launch_bwd(const BwdCall& c, const typename OP::elem* qt, const typename OP:
     TimedLaunch timed(SA_KERNEL_BACKWARD_DQ, c.st);
     if constexpr (sizeof(elem) == 2 && D == 64 && G == 1) {   // one head per wavefront: the pipelined kernel
       const dim3 grid64((unsigned)cdiv(c.T, DQ64_WAVES * TILE), (unsigned)(c.nseq * c.H));
-#define SA_LAUNCH_DQ64(CVV, SOLO)                                                                                  \
-  hipLaunchKernelGGL((bwd_dq64_kernel<CVV, SOLO>), grid64, dim3(DQ64_WAVES * 64), 0, c.st, q, k, v, dout, c.qs, c.ks, \
-                     c.vs, c.dos, lse, dbar, c.carry, ucheck, dq0h, dq0x, dqv, c.nseq, c.H, c.T, ldt, c.exempt,    \
-                     c.scale)
+#define SA_LAUNCH_DQ64(CVV, SOLO, SNAKE)                                                                           \
+  hipLaunchKernelGGL((bwd_dq64_kernel<CVV, SOLO, SNAKE>), grid64, dim3(DQ64_WAVES * 64), 0, c.st, q, k, v, dout, c.qs, \
+                     c.ks, c.vs, c.dos, lse, dbar, c.carry, ucheck, dq0h, dq0x, dqv, c.nseq, c.H, c.T, ldt, c.exempt, \
+                     c.scale, dq_slots)
+      const int dq_slots = bwd_snake_slots((int64_t)grid64.x * grid64.y, 1, device_cus());
       if (c.H == 1) {   // one-head sequences: head 0's loop only
-        if (cv) SA_LAUNCH_DQ64(true, true);
-        else SA_LAUNCH_DQ64(false, true);
+        if (cv) SA_LAUNCH_DQ64(true, true, false);
+        else SA_LAUNCH_DQ64(false, true, false);
+      } else if (dq_slots > 0) {
+        if (cv) SA_LAUNCH_DQ64(true, false, true);
+        else SA_LAUNCH_DQ64(false, false, true);
       } else {
-        if (cv) SA_LAUNCH_DQ64(true, false);
-        else SA_LAUNCH_DQ64(false, false);
+        if (cv) SA_LAUNCH_DQ64(true, false, false);
+        else SA_LAUNCH_DQ64(false, false, false);
       }
 #undef SA_LAUNCH_DQ64
     } else {

@@ -110,3 +110,25 @@ def test_repeated_chunked_prefill_is_bit_identical(cuda):
     for out, state in results[1:]:
         assert torch.equal(results[0][0], out)
         assert torch.equal(results[0][1], state)
+
+
+def test_batched_equals_each_sequence_alone(cuda):
+    """A sequence's outputs and gradients do not depend on what else shares its launch: 8 sequences of
+    12 heads in one call equal each sequence run alone, bit for bit. The batched call is sized so that
+    its query-side backward holds 2.7-3 workgroups per CU slot, where that kernel deals its workgroups
+    to the XCDs in the order of work_order_block(slots) (shortest third after the first round); the
+    single-sequence calls fill less than one round and take the longest-first order, and their
+    forward runs one head per wavefront where the batched one runs two. A dispatch order that lost or
+    repeated a workgroup, or a result that depended on the order, would show here."""
+    b, h, t, d = 8, 12, 2048, 64
+    cus = torch.cuda.get_device_properties(cuda).multi_processor_count
+    rounds = (t // 256) * b * h / ((cus // 8) * 8)
+    print(f"case batched vs alone B={b} H={h} T={t}: query-side rounds {rounds:.2f}", flush=True)
+    assert 2.7 <= rounds <= 3.0, rounds   # (the regime this test is for, on an MI355X's 256 CUs)
+    q, k, v, do = _inputs((b, h, t, d), seed=12, cuda=cuda)
+    whole = _fwd_bwd(q, k, v, do)
+    for i in range(b):
+        sl = slice(i, i + 1)
+        alone = _fwd_bwd(q[sl].contiguous(), k[sl].contiguous(), v[sl].contiguous(), do[sl].contiguous())
+        for name, x, y in zip(("out", "dq", "dk", "dv"), whole, alone):
+            assert torch.equal(x[sl], y), (i, name)
