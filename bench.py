@@ -51,15 +51,15 @@ KERNEL_FLOP = {"forward": 2.0 * UNIT, "backward_kv": 4.0 * UNIT, "backward_dq": 
 # 1.0): profiles/c2_attention_kernels_traffic.md. The counters need the profiler, so bench.py
 # reports the committed measurement, labelled with the hash of the kernel sources it was taken on
 # (PROFILED_SOURCES): the line says whether the sources it runs are still those.
-MEASURED_TRAFFIC_BYTES = {"forward": (2.0 * 436_267 + 67_585) * 1024,
-                          "backward_kv": (2.0 * 331_656 + 391_685) * 1024,
-                          "backward_dq": (2.0 * 355_509 + 96_256) * 1024}
+MEASURED_TRAFFIC_BYTES = {"forward": (2.0 * 460_700 + 67_588) * 1024,
+                          "backward_kv": (2.0 * 330_872 + 391_687) * 1024,
+                          "backward_dq": (2.0 * 352_457 + 96_256) * 1024}
 # C4 (131072-token prefill, 8 chunks): the forward kernel's HBM bytes per launch (mean over the
 # chunks, FETCH_SIZE x 2.0 + WRITE_SIZE x 1.0) and MFMA busy fraction, measured with rocprofv3:
 # profiles/c4_prefill_kernels.md. The run's own per-launch time turns the bytes into a rate.
-MEASURED_C4 = {"hbm_bytes_per_launch": (2.0 * 3_266_201 + 67_584) * 1024, "mfma_busy": 0.35}
+MEASURED_C4 = {"hbm_bytes_per_launch": (2.0 * 3_288_204 + 67_584) * 1024, "mfma_busy": 0.35}
 # sha256 (first 16 hex digits) of csrc/sa_kernels.h when the figures above were profiled
-PROFILED_SOURCES = "27eada1fbe1d7ad8"
+PROFILED_SOURCES = "686b814c501d5591"
 KERNEL_SOURCE = os.path.join(ROOT, "selective-attention-study_amd", "csrc", "sa_kernels.h")
 
 
