@@ -197,3 +197,23 @@ def test_fwd64_one_or_two_heads_per_wavefront_same_bits(cuda, batch, heads, seq,
         with torch.no_grad():
             want = sa_oracle.attention(q.double(), k.double(), v.double(), exempt)
         assert (runs[0][0].cpu().double() - want).abs().max().item() < 3e-2
+
+
+def test_fwd64_prefill_widths_same_bits(cuda):
+    """The chunked prefill (a query offset, keys of earlier chunks, a carried per-key state) gives the
+    same bits and the same state at one and two heads per wavefront and with the automatic choice
+    (one head per wavefront here: each chunk's grid fills the CUs less than once)."""
+    b, h, t, chunk = 2, 6, 3072, 1024
+    print(f"case fwd64 prefill widths B={b} H={h} T={t} chunk={chunk}", flush=True)
+    q, k, v, _ = _inputs(b, h, t, 64, seed=61, scale=1.2)
+    qd, kd, vd = (x.to(cuda) for x in (q, k, v))
+    runs = []
+    for g in (1, 2, None):
+        state = torch.zeros(b, t, device=cuda)
+        outs = [kernels.selective_attention_prefill(qd[:, :, c0:c0 + chunk], kd[:, :, :c0 + chunk],
+                                                    vd[:, :, :c0 + chunk], state, c0, group=g)
+                for c0 in range(0, t, chunk)]
+        runs.append((torch.cat(outs, dim=2), state))
+    for out, state in runs[1:]:
+        assert torch.equal(out, runs[0][0])
+        assert torch.equal(state, runs[0][1])
