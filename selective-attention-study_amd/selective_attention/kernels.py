@@ -474,7 +474,12 @@ def selective_attention_decode(
         raise ValueError(f"q (B, H, D) and k, v (B, H, t, D) must all be with matching B, H, D; "
                          f"got {tuple(q.shape)}, {tuple(k.shape)}, {tuple(v.shape)}")
     check_inputs(k, k, v)
-    check_inputs(q[:, :, None], q[:, :, None], q[:, :, None])
+    # q's own checks (its head dim equals k's, checked above), without building the 4-D views
+    # check_inputs takes: a decode step is host-bound at short caches, so its checks stay cheap
+    if not (q.is_cuda and q.device == k.device):
+        raise ValueError("q, k, v must be CUDA (ROCm) tensors on one device")
+    if q.dtype not in DTYPES:
+        raise ValueError(f"dtype must be float16, bfloat16 or float32; got {q.dtype}, {k.dtype}, {v.dtype}")
     exempt = _check_exempt(exempt)
     batch, heads, t, head_dim = k.shape
     if (selected.dim() != 3 or selected.shape[0] != batch or heads % selected.shape[1] != 0
@@ -496,10 +501,17 @@ def selective_attention_decode(
         kstride = t * kdim
     out = torch.empty(batch, heads, kdim, device=dev, dtype=torch.float32)
     ws = torch.empty(max(int(lib.sa_decode_workspace_bytes(batch, heads, t, kdim)), 1), device=dev, dtype=torch.uint8)
-    with torch.cuda.device(dev):
+    def launch():
         _lib.check(lib.sa_decode(qs.data_ptr(), ks.data_ptr(), vs.data_ptr(), out.data_ptr(), selected.data_ptr(),
                                  selected.stride(1), ws.data_ptr(), ws.numel(), batch, heads, groups, t, kstride,
                                  kdim, 1.0 / math.sqrt(head_dim), code, exempt, _stream(dev)))
+
+    # (a device guard only when q's device is not already the current one: it costs a few us a step)
+    if dev.index == torch.cuda.current_device():
+        launch()
+    else:
+        with torch.cuda.device(dev):
+            launch()
     return out[..., :head_dim]
 
 
